@@ -1,0 +1,211 @@
+/*
+ * spirv_hip.h — C ABI of the MI355X (gfx950) operator-kernel library.
+ *
+ * This is the drop-in boundary for the operator-dispatch layer of
+ * agkdc1/SPIRV_INFERENCE.  The reference crosses the device boundary through
+ *   tflite_loader::vulkan::run_kernel(device_selector, &KernelRun) -> KernelOutput
+ *   (source/tflite_loader/src/vulkan.rs:27-44)
+ * which creates a Vulkan device, uploads, dispatches one SPIR-V module chosen by
+ * name (source/tflite_loader/src/kernels.rs:12-238), waits and reads back on every
+ * call.  Here the kernel is still chosen by the reference's kernel name and driven by
+ * the exact i32 push-constant vector of that kernel's `Params` block, but the device,
+ * stream and tensors are created once and stay resident in HBM.
+ *
+ * Plain C: no HIP or torch types in any signature.  Every entry point returns
+ * SHP_OK (0) or a negative SHP_ERR_* code; shp_last_error() gives a thread-local
+ * message.  Unknown kernels, short push vectors and inconsistent sizes are errors,
+ * never a silent fallback (mirrors the fail-closed `bail!` of
+ * source/tflite_loader/src/scheduler.rs:1003-1007).
+ *
+ * One context = one HIP stream on one device.  A context is not thread-safe.
+ * shp_launch* are asynchronous on the context stream; shp_run_kernel is synchronous.
+ */
+#ifndef SPIRV_HIP_H
+#define SPIRV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------- */
+#define SHP_OK 0
+#define SHP_ERR_INVALID (-1)        /* null pointer / bad argument */
+#define SHP_ERR_UNKNOWN_KERNEL (-2) /* name not in the registry */
+#define SHP_ERR_PUSH (-3)           /* push vector shorter than the kernel's Params */
+#define SHP_ERR_SHAPE (-4)          /* sizes inconsistent with the push vector */
+#define SHP_ERR_HIP (-5)            /* HIP runtime error */
+#define SHP_ERR_NO_DEVICE (-6)      /* selector matched no device */
+#define SHP_ERR_UNSUPPORTED (-7)    /* configuration the kernel does not handle */
+
+/* ---- types ----------------------------------------------------------------- */
+typedef struct shp_ctx shp_ctx;
+
+/* Replaces KernelOutput (source/tflite_loader/src/vulkan.rs:18-25).  The values
+ * vector is written into the caller's `out` buffer instead of being returned. */
+typedef struct shp_run_info {
+    char device_name[256];
+    uint32_t vendor_id; /* 0x1002 for AMD */
+    uint32_t device_id;
+    double elapsed_ms; /* hipEvent pair around the dispatch (kernel time only) */
+} shp_run_info;
+
+/* Fused activations applied in kernel epilogues.  The reference applies them as a
+ * separate post-op dispatch (apply_activation, source/tflite_loader/src/scheduler.rs:1146-1197). */
+enum {
+    SHP_ACT_NONE = 0,
+    SHP_ACT_RELU = 1,     /* relu.comp: max(x, 0) */
+    SHP_ACT_RELU6 = 2,    /* relu6.comp: min(max(x, 0), 6) */
+    SHP_ACT_LEAKY = 3,    /* leaky_relu.comp: max(alpha*x, x) */
+    SHP_ACT_SIGMOID = 4,  /* sigmoid.comp: 1/(1+exp(-x)) */
+    SHP_ACT_TANH = 5,     /* tanh.comp: clamp to +-20, (e^x-e^-x)/(e^x+e^-x) */
+    SHP_ACT_SILU = 6,     /* x*sigmoid(x) (export_llama.py:298-299) */
+    SHP_ACT_GELU_ERF = 7  /* 0.5*x*erfc(-x/sqrt(2)) (bert_base.stablehlo.txt:16-17) */
+};
+
+/* Epilogue of the dense and depthwise kernels: out = act(acc + bias[c] + residual).
+ * `bias` is indexed by the output channel (last NHWC dim, the OC of NCHW, or the
+ * column of a GEMM); `residual` has the layout of `out`.  Either may be NULL. */
+typedef struct shp_epilogue {
+    const float* bias;
+    const float* residual;
+    int32_t act;
+    float alpha;
+} shp_epilogue;
+
+/* ---- context / device (device selection: vulkan.rs:204-231) ----------------- */
+
+/* selector: "any", "amd", or a decimal device ordinal ("0").  Reports vendor 0x1002. */
+int shp_create(const char* selector, shp_ctx** out);
+void shp_destroy(shp_ctx* ctx);
+const char* shp_last_error(void);
+int shp_device_info(shp_ctx* ctx, shp_run_info* info);
+/* Run the context's work on an external hipStream_t (NULL = the context's own). */
+int shp_set_stream(shp_ctx* ctx, void* hip_stream);
+void* shp_get_stream(shp_ctx* ctx);
+
+/* ---- resident tensors (new: the reference re-uploads per op, vulkan.rs:109-112,172) */
+int shp_alloc(shp_ctx* ctx, size_t bytes, void** dptr);
+int shp_free(shp_ctx* ctx, void* dptr);
+int shp_upload(shp_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+int shp_download(shp_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+int shp_sync(shp_ctx* ctx);
+
+/* Deterministic counter-based fill used for the synthetic inputs and random-init
+ * weights of the benchmark configs: value i of tensor `tensor_id` depends only on
+ * (seed, tensor_id, i).  kind 0: uniform [lo, hi); kind 1: normal(mean=lo, std=hi). */
+int shp_fill_random(shp_ctx* ctx, float* dptr, uint64_t n, uint64_t seed, uint64_t tensor_id,
+                    int32_t kind, float lo, float hi);
+
+/* ---- kernel registry (source/tflite_loader/src/kernels.rs:12-257) ------------ */
+int shp_kernel_count(void);
+const char* shp_kernel_name(int index);
+/* Number of i32 push constants of the kernel's Params block, or <0 if unknown. */
+int shp_kernel_push_count(const char* kernel);
+
+/* ---- dispatch ----------------------------------------------------------------- */
+
+/* Device-pointer launch: the three-binding ABI of every .comp kernel
+ * (binding 0 = in0, 1 = in1/weights, 2 = out) plus its i32 push vector.  Replaces the
+ * KernelRun of vulkan.rs:27-36; `out_elems` is the KernelRun::output_elements. */
+int shp_launch(shp_ctx* ctx, const char* kernel, const void* in0, const void* in1, void* out,
+               const int32_t* push, size_t n_push, uint64_t out_elems);
+
+/* As shp_launch, with a fused epilogue (bias / residual / activation). */
+int shp_launch_ex(shp_ctx* ctx, const char* kernel, const void* in0, const void* in1, void* out,
+                  const int32_t* push, size_t n_push, uint64_t out_elems,
+                  const shp_epilogue* epi);
+
+/* Host-to-host synchronous call with the semantics of
+ * run_kernel(device_selector, &KernelRun) (source/tflite_loader/src/vulkan.rs:42-44):
+ * upload in0[n0], in1[n1], dispatch, wait, download out[n_out].  grid_hint (the
+ * reference's dispatch_x) is advisory.  `info` may be NULL. */
+int shp_run_kernel(shp_ctx* ctx, const char* kernel, const float* in0, size_t n0,
+                   const float* in1, size_t n1, float* out, size_t n_out, const int32_t* push,
+                   size_t n_push, uint32_t grid_hint, shp_run_info* info);
+
+/* ---- per-launch timing (the reference's KernelOutput.elapsed_ms, vulkan.rs:163-171) */
+/* When enabled, every launch is bracketed by hipEvents on the context stream and
+ * accumulated per kernel name. */
+int shp_timing_enable(shp_ctx* ctx, int enable);
+int shp_timing_reset(shp_ctx* ctx);
+/* Fills name/total ms/count of entry `index` (synchronises first). */
+int shp_timing_entry(shp_ctx* ctx, int index, char* name, size_t name_cap, double* total_ms,
+                     uint64_t* count);
+
+/* ---- resident op graphs: the chained runtime (runtime/chained_graph_runtime/src/main.rs:260-590)
+ *      generalised, and the model drivers of the benchmark configs ---------------- */
+typedef struct shp_model shp_model;
+
+/* arch: "resnet50_v1_5" (HLO path, NHWC/HWIO, BN folded), "mobilenet_v2",
+ * "efficientnet_lite0" (TFLite path), "bert_base".  seq_len only for bert_base.
+ * Weights are filled with shp_fill_random(seed) per the config's init rule. */
+int shp_model_create(shp_ctx* ctx, const char* arch, int32_t batch, int32_t seq_len,
+                     uint64_t seed, shp_model** out);
+void shp_model_destroy(shp_model* model);
+/* Enqueue one forward pass of every op on the context stream. */
+int shp_model_run(shp_model* model);
+/* Capture the op list into a hipGraph once and replay it on later runs. */
+int shp_model_use_graph(shp_model* model, int enable);
+int shp_model_input(shp_model* model, int index, void** dptr, uint64_t* elems);
+int shp_model_output(shp_model* model, int index, void** dptr, uint64_t* elems);
+/* Algorithmic work of one forward pass: 2*MAC of convs/GEMMs, and weight bytes. */
+int shp_model_work(shp_model* model, double* flops, double* weight_bytes);
+
+/* Op-list introspection: lets a checker replay every op on other hardware. */
+typedef struct shp_op_desc {
+    char kernel[64];
+    int32_t push[40];
+    int32_t n_push;
+    int32_t in0, in1, out;   /* tensor ids (-1 = none) */
+    int32_t bias, residual;  /* epilogue tensor ids (-1 = none) */
+    int32_t act;
+    float alpha;
+    uint64_t out_elems;
+    char label[64];
+} shp_op_desc;
+int shp_model_num_ops(shp_model* model);
+int shp_model_op(shp_model* model, int index, shp_op_desc* desc);
+int shp_model_num_tensors(shp_model* model);
+/* kind: 0 activation, 1 weight/constant, 2 model input */
+int shp_model_tensor(shp_model* model, int id, void** dptr, uint64_t* elems, int32_t* kind);
+
+/* ---- TinyLlama-shaped greedy decode with a KV cache (export_llama.py:269-375 math,
+ *      run_llama_spirv.py:194-295 loop, without the full S=64 recompute) ----------- */
+typedef struct shp_llama shp_llama;
+typedef struct shp_llama_config {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+    float rms_eps, rope_theta;
+} shp_llama_config;
+
+int shp_llama_create(shp_ctx* ctx, const shp_llama_config* cfg, uint64_t seed,
+                     shp_llama** out);
+void shp_llama_destroy(shp_llama* lm);
+/* Clears the KV cache and the position counter. */
+int shp_llama_reset(shp_llama* lm);
+/* Runs one token at the current position (KV cache append), writes logits to the
+ * device logits buffer and the greedy argmax (lowest index on ties) to the device
+ * token slot; advances the position. Asynchronous. */
+int shp_llama_step(shp_llama* lm, int32_t token);
+/* Feeds prompt[0..n_prompt) then generates n_new greedy tokens into out_tokens
+ * (synchronous).  Stops early at token 2 (EOS) or 0 (PAD) like run_llama_spirv.py:292-294;
+ * returns the number written through *n_out. */
+int shp_llama_generate(shp_llama* lm, const int32_t* prompt, int32_t n_prompt, int32_t n_new,
+                       int32_t* out_tokens, int32_t* n_out);
+int shp_llama_use_graph(shp_llama* lm, int enable);
+int shp_llama_logits(shp_llama* lm, void** dptr, uint64_t* elems);
+/* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head",
+ * or per layer "attn_norm","wq","wk","wv","wo","ffn_norm","w_gate","w_up","w_down".
+ * Projection matrices are stored row-major [out,in], the transpose of export_llama.py's
+ * [in,out] (`.T` at :203-217,238): one output's weights are contiguous for the GEMV. */
+int shp_llama_weight(shp_llama* lm, int32_t layer, const char* which, void** dptr,
+                     uint64_t* elems);
+int shp_llama_weight_bytes(shp_llama* lm, double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPIRV_HIP_H */

@@ -1,0 +1,131 @@
+// Internal declarations shared by the kernel translation units and the runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "spirv_hip.h"
+
+namespace shp {
+
+// Thread-local error message behind shp_last_error().
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define SHP_HIP_CHECK(expr)                                                           \
+    do {                                                                              \
+        hipError_t e__ = (expr);                                                      \
+        if (e__ != hipSuccess)                                                        \
+            return ::shp::fail(SHP_ERR_HIP, std::string(#expr " failed: ") +          \
+                                                hipGetErrorString(e__));             \
+    } while (0)
+
+// Everything a launcher needs: the three bindings, the push vector and the epilogue.
+struct Launch {
+    hipStream_t stream;
+    const void* in0;
+    const void* in1;
+    void* out;
+    const int32_t* push;
+    size_t n_push;
+    uint64_t out_elems;
+    const shp_epilogue* epi;  // never null inside launchers (zero epilogue if absent)
+    float* workspace;         // context-owned scratch (split-K partials), may be null
+    size_t workspace_bytes;
+};
+
+using LaunchFn = int (*)(const Launch&);
+
+struct KernelEntry {
+    const char* name;
+    int n_push;        // i32 count of the Params block
+    bool epilogue_ok;  // accepts bias/residual/activation
+    LaunchFn fn;
+};
+
+// Registry tables, one per translation unit; registry.cpp concatenates them.
+extern KernelEntry kElementwiseKernels[];
+extern const int kElementwiseKernelCount;
+extern KernelEntry kReduceKernels[];
+extern const int kReduceKernelCount;
+extern KernelEntry kGemmKernels[];
+extern const int kGemmKernelCount;
+extern KernelEntry kSpatialKernels[];
+extern const int kSpatialKernelCount;
+extern KernelEntry kDecodeKernels[];
+extern const int kDecodeKernelCount;
+
+const KernelEntry* find_kernel(const char* name);
+
+// Launch a registered kernel on a stream (used by the graph runtime and the models).
+int launch_kernel(hipStream_t stream, const char* name, const void* in0, const void* in1,
+                  void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
+                  const shp_epilogue* epi, float* workspace, size_t workspace_bytes);
+
+// Counter-based RNG fill (kernels_elementwise.hip).
+int fill_random(hipStream_t stream, float* p, uint64_t n, uint64_t seed, uint64_t tensor_id,
+                int kind, float lo, float hi);
+
+inline unsigned grid_1d(uint64_t n, unsigned block) {
+    uint64_t g = (n + block - 1) / block;
+    return g == 0 ? 1u : (unsigned)g;
+}
+
+// Shape check helper for launchers.
+inline int check_total(const Launch& l, int64_t expect, const char* kernel) {
+    if (expect < 0 || (uint64_t)expect != l.out_elems)
+        return fail(SHP_ERR_SHAPE, std::string(kernel) + ": push-vector total " +
+                                       std::to_string(expect) + " != output elements " +
+                                       std::to_string(l.out_elems));
+    return SHP_OK;
+}
+
+}  // namespace shp
+
+// ---- device-side helpers --------------------------------------------------------
+namespace shpd {
+
+// erfc(z) as the XLA rational expansion the BERT fixture spells out op by op
+// (source/xla_hlo/fixtures/bert_base.stablehlo.txt:59-144): a polynomial in z^2 for
+// |z| <= 1, exp(-z^2)*P(1/z^2)/(min(|z|,10.06)*Q(1/z^2)) otherwise, reflected for z < 0.
+__device__ __forceinline__ float erfc_xla(float z) {
+    float az = fabsf(z);
+    if (az > 1.0f) {
+        float z2 = z * z;
+        float e = expf(-z2);
+        float q = 1.0f / z2;
+        float p = ((0.102081165f * q + 0.429206669f) * q + 0.323790789f) * q + 0.053971976f;
+        float d = ((((0.0172516778f * q + 0.391371638f) * q + 1.0f) * q + 0.621732414f) * q +
+                   0.0956628621f);
+        float r = e * (p / (fminf(az, 10.06f) * d));
+        return z < 0.0f ? 2.0f - r : r;
+    }
+    float w = z * z;
+    float s = ((((0.000561802299f * w - 0.00491381669f) * w + 0.0267075151f) * w -
+                0.112800106f) * w + 0.376122952f) * w - 1.12837911f;
+    return z * s + 1.0f;
+}
+
+__device__ __forceinline__ float apply_act(float x, int act, float alpha) {
+    switch (act) {
+        case SHP_ACT_RELU: return fmaxf(x, 0.0f);
+        case SHP_ACT_RELU6: return fminf(fmaxf(x, 0.0f), 6.0f);
+        case SHP_ACT_LEAKY: return fmaxf(alpha * x, x);
+        case SHP_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
+        case SHP_ACT_TANH: {
+            float c = fminf(fmaxf(x, -20.0f), 20.0f);
+            float ep = expf(c), en = expf(-c);
+            return (ep - en) / (ep + en);
+        }
+        case SHP_ACT_SILU: return x * (1.0f / (1.0f + expf(-x)));
+        case SHP_ACT_GELU_ERF: return (0.5f * x) * erfc_xla(-x * 0.707106769f);
+        default: return x;
+    }
+}
+
+}  // namespace shpd

@@ -1,0 +1,800 @@
+// Dense contractions on the fp32 matrix cores of gfx950 (v_mfma_f32_32x32x2_f32).
+//
+// One implicit-GEMM kernel template serves every dense kernel of the reference:
+//   hlo_conv_nhwc_hwio  kernels/hlo_conv_nhwc_hwio/glsl/hlo_conv_nhwc_hwio.comp:25-49
+//                       (host: source/xla_hlo/src/compiler.rs:768-855)
+//   conv2d              kernels/conv2d/glsl/conv2d.comp:26-50 (NCHW, OIHW + bias tail,
+//                       host: source/tflite_loader/src/scheduler.rs:321-427,1327-1362)
+//   fully_connected     kernels/fully_connected/glsl/fully_connected.comp:15-28 ([out,in] +
+//                       bias tail, host: scheduler.rs:914-1002,1402-1436)
+//   hlo_dot_batched     kernels/hlo_dot_batched/glsl/hlo_dot_batched.comp:19-38
+//   hlo_dot_rank2       kernels/hlo_dot_rank2/glsl/hlo_dot_rank2.comp:15-26
+// The reference computes one output per invocation with a serial K loop and no tiling.
+// Here a 256-thread workgroup (4 wavefronts) owns a BM x BN output tile; K advances in
+// tiles of 32 staged through LDS with double buffering; each wavefront accumulates
+// FM x FN blocks of 32x32 in the MFMA accumulators.  A and B are read in place in
+// whatever layout the caller has (NHWC im2col, NCHW im2col, row-major, transposed,
+// strided batch), so no host-side permutes (compiler.rs:1043-1058) are needed.  The
+// epilogue fuses bias, residual and activation; K can be split across workgroups with a
+// deterministic second pass when the tile grid alone cannot fill 256 CUs.
+#include "gemm.h"
+
+namespace {
+
+using shp::GemmParams;
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 32;      // K tile
+constexpr int KTAB = 1024;  // im2col offset table entries (scalar conv modes)
+
+struct ConvRow {
+    int64_t base;  // element offset of tap (0,0) of this output pixel (may be "negative")
+    int iy0, ix0;  // top-left input coordinate of the window
+    bool valid;
+};
+
+__device__ __forceinline__ ConvRow conv_row(const GemmParams& p, int m, int amode) {
+    ConvRow r;
+    r.valid = m < p.M;
+    int mm = r.valid ? m : 0;
+    int ox = mm % p.cow;
+    int t = mm / p.cow;
+    int oy = t % p.coh;
+    int img = t / p.coh;
+    r.iy0 = oy * p.csh - p.cpt;
+    r.ix0 = ox * p.csw - p.cpl;
+    if (amode == shp::A_CONV_NCHW) {
+        r.base = (int64_t)img * p.cic * p.cih * p.ciw + (int64_t)r.iy0 * p.ciw + r.ix0;
+    } else {
+        r.base = (int64_t)img * p.cih * p.ciw * p.cic +
+                 ((int64_t)r.iy0 * p.ciw + r.ix0) * p.cic;
+    }
+    return r;
+}
+
+// Decompose a K index of a convolution into (element offset, ky, kx).
+__device__ __forceinline__ void conv_k(const GemmParams& p, int k, int amode, int& off, int& ky,
+                                       int& kx) {
+    if (amode == shp::A_CONV_NCHW) {  // k = (ic, ky, kx)
+        kx = k % p.ckw;
+        int t = k / p.ckw;
+        ky = t % p.ckh;
+        int ic = t / p.ckh;
+        off = (ic * p.cih + ky) * p.ciw + kx;
+    } else {  // k = (ky, kx, ic)
+        int ic = k % p.cic;
+        int t = k / p.cic;
+        kx = t % p.ckw;
+        ky = t / p.ckw;
+        off = (ky * p.ciw + kx) * p.cic + ic;
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int AM, int BMD, int CM>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+    constexpr int FM = BM / WM / 32;
+    constexpr int FN = BN / WN / 32;
+    static_assert(WM * WN == 4, "four wavefronts per workgroup");
+    static_assert(FM >= 1 && FN >= 1, "tile too small for 32x32 blocks");
+    constexpr bool A_VEC = (AM == shp::A_KVEC || AM == shp::A_CONV_NHWC4);
+    constexpr bool A_CONV = (AM == shp::A_CONV_NHWC4 || AM == shp::A_CONV_NHWC ||
+                             AM == shp::A_CONV_NCHW);
+    constexpr bool A_TAB = (AM == shp::A_CONV_NHWC || AM == shp::A_CONV_NCHW);
+    constexpr int NA = A_VEC ? BM / 32 : BM / 8;              // A loads per thread
+    constexpr int NB = (BMD == shp::B_STRIDED) ? BN / 8 : BN / 32;  // B loads per thread
+    constexpr int AP = 4, BP = 4;
+
+    __shared__ __attribute__((aligned(16))) float As[2][BM][BK + AP];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][BN + BP];
+    __shared__ int2 ktab[A_TAB ? KTAB : 1];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 31, lh = lane >> 5;
+
+    // ---- tile coordinates: give each XCD (block id mod 8) a contiguous run of tiles so
+    // the workgroups sharing A rows / B columns meet in the same L2.
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int ntiles = tiles_m * tiles_n;
+    int bid = blockIdx.x;
+    const int full = (ntiles / 8) * 8;
+    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+    const int tm = bid / tiles_n, tn = bid % tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int split = blockIdx.y;
+    const int bz = blockIdx.z;
+    const int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
+    const float* __restrict__ A = p.a + bo * p.sa_outer + bi * p.sa_inner;
+    const float* __restrict__ B = p.b + bo * p.sb_outer + bi * p.sb_inner;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int ntk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    // ---- per-thread load coordinates
+    // A: vector modes -> row = tid/8 + 32*j, kq = (tid%8)*4; scalar modes -> m = tid%BM,
+    //    k = tid/BM + (256/BM)*j.
+    ConvRow crow[A_CONV ? (A_VEC ? NA : 1) : 1];
+    if constexpr (A_CONV) {
+        if constexpr (A_VEC) {
+#pragma unroll
+            for (int j = 0; j < NA; ++j) crow[j] = conv_row(p, m0 + tid / 8 + 32 * j, AM);
+        } else {
+            crow[0] = conv_row(p, m0 + tid % BM, AM);
+        }
+    }
+    if constexpr (A_TAB) {
+        // offsets of every K index this workgroup visits, when they fit the table
+        int span = kend - kbeg;
+        if (span <= KTAB) {
+            for (int k = tid; k < span; k += 256) {
+                int off, ky, kx;
+                conv_k(p, kbeg + k, AM, off, ky, kx);
+                ktab[k] = make_int2(off, (ky << 16) | kx);
+            }
+        }
+        __syncthreads();
+    }
+
+    float4 ra[A_VEC ? NA : 1];
+    float rs[A_VEC ? 1 : NA];
+    float4 rb[BMD == shp::B_STRIDED ? 1 : NB];
+    float rbs[BMD == shp::B_STRIDED ? NB : 1];
+
+    auto load_a = [&](int kt) {
+        const int kt0 = kbeg + kt * BK;
+        if constexpr (A_VEC) {
+            const int kq = (tid & 7) * 4;
+            const int k = kt0 + kq;
+            if constexpr (AM == shp::A_KVEC) {
+#pragma unroll
+                for (int j = 0; j < NA; ++j) {
+                    int m = m0 + tid / 8 + 32 * j;
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (m < p.M && k < kend)
+                        v = *reinterpret_cast<const float4*>(A + (int64_t)m * p.sam + k);
+                    ra[j] = v;
+                }
+            } else {  // A_CONV_NHWC4
+                int off = 0, ky = 0, kx = 0;
+                if (k < kend) conv_k(p, k, AM, off, ky, kx);
+#pragma unroll
+                for (int j = 0; j < NA; ++j) {
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    int iy = crow[j].iy0 + ky, ix = crow[j].ix0 + kx;
+                    if (crow[j].valid && k < kend && iy >= 0 && iy < p.cih && ix >= 0 &&
+                        ix < p.ciw)
+                        v = *reinterpret_cast<const float4*>(A + crow[j].base + off);
+                    ra[j] = v;
+                }
+            }
+        } else {
+            const int ml = tid % BM;
+            const int m = m0 + ml;
+#pragma unroll
+            for (int j = 0; j < NA; ++j) {
+                int kl = tid / BM + (256 / BM) * j;
+                int k = kt0 + kl;
+                float v = 0.f;
+                if constexpr (AM == shp::A_STRIDED) {
+                    if (m < p.M && k < kend) v = A[(int64_t)m * p.sam + (int64_t)k * p.sak];
+                } else {
+                    if (crow[0].valid && k < kend) {
+                        int off, ky, kx;
+                        if (kend - kbeg <= KTAB) {
+                            int2 e = ktab[k - kbeg];
+                            off = e.x;
+                            ky = e.y >> 16;
+                            kx = e.y & 0xffff;
+                        } else {
+                            conv_k(p, k, AM, off, ky, kx);
+                        }
+                        int iy = crow[0].iy0 + ky, ix = crow[0].ix0 + kx;
+                        if (iy >= 0 && iy < p.cih && ix >= 0 && ix < p.ciw)
+                            v = A[crow[0].base + off];
+                    }
+                }
+                rs[j] = v;
+            }
+        }
+    };
+
+    auto store_a = [&](int buf) {
+        if constexpr (A_VEC) {
+            const int kq = (tid & 7) * 4;
+#pragma unroll
+            for (int j = 0; j < NA; ++j)
+                *reinterpret_cast<float4*>(&As[buf][tid / 8 + 32 * j][kq]) = ra[j];
+        } else {
+            const int ml = tid % BM;
+#pragma unroll
+            for (int j = 0; j < NA; ++j) As[buf][ml][tid / BM + (256 / BM) * j] = rs[j];
+        }
+    };
+
+    auto load_b = [&](int kt) {
+        const int kt0 = kbeg + kt * BK;
+        if constexpr (BMD == shp::B_NVEC) {
+            constexpr int TPR = BN / 4;  // threads per k row
+            const int n = n0 + (tid % TPR) * 4;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                int k = kt0 + tid / TPR + (256 / TPR) * j;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k < kend && n < p.N)
+                    v = *reinterpret_cast<const float4*>(B + (int64_t)k * p.sbk + n);
+                rb[j] = v;
+            }
+        } else if constexpr (BMD == shp::B_KVEC) {
+            const int n = n0 + tid % BN;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                int k = kt0 + (tid / BN) * 4 + (256 / BN) * 4 * j;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k < kend && n < p.N)
+                    v = *reinterpret_cast<const float4*>(B + (int64_t)n * p.sbn + k);
+                rb[j] = v;
+            }
+        } else {
+            const int n = n0 + tid % BN;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                int k = kt0 + tid / BN + (256 / BN) * j;
+                float v = 0.f;
+                if (k < kend && n < p.N) v = B[(int64_t)k * p.sbk + (int64_t)n * p.sbn];
+                rbs[j] = v;
+            }
+        }
+    };
+
+    auto store_b = [&](int buf) {
+        if constexpr (BMD == shp::B_NVEC) {
+            constexpr int TPR = BN / 4;
+            const int nl = (tid % TPR) * 4;
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                *reinterpret_cast<float4*>(&Bs[buf][tid / TPR + (256 / TPR) * j][nl]) = rb[j];
+        } else if constexpr (BMD == shp::B_KVEC) {
+            const int nl = tid % BN;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                int kl = (tid / BN) * 4 + (256 / BN) * 4 * j;
+                Bs[buf][kl + 0][nl] = rb[j].x;
+                Bs[buf][kl + 1][nl] = rb[j].y;
+                Bs[buf][kl + 2][nl] = rb[j].z;
+                Bs[buf][kl + 3][nl] = rb[j].w;
+            }
+        } else {
+            const int nl = tid % BN;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) Bs[buf][tid / BN + (256 / BN) * j][nl] = rbs[j];
+        }
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int arow = wm * (BM / WM) + li;
+    const int bcol = wn * (BN / WN) + li;
+
+    if (ntk > 0) {
+        load_a(0);
+        load_b(0);
+        store_a(0);
+        store_b(0);
+        __syncthreads();
+        for (int kt = 0; kt < ntk; ++kt) {
+            const int buf = kt & 1;
+            if (kt + 1 < ntk) {
+                load_a(kt + 1);
+                load_b(kt + 1);
+            }
+            // Lanes 0-31 feed k = s, lanes 32-63 feed k = 16 + s of this K tile: any
+            // assignment works as long as A and B agree, and this one lets each lane read
+            // 16 consecutive k of its A row with 128-bit LDS loads.
+#pragma unroll
+            for (int s4 = 0; s4 < BK / 8; ++s4) {
+                float4 af[FM];
+                float bf[FN][4];
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+                    af[fm] = *reinterpret_cast<const float4*>(
+                        &As[buf][arow + fm * 32][lh * 16 + s4 * 4]);
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        bf[fn][q] = Bs[buf][lh * 16 + s4 * 4 + q][bcol + fn * 32];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn) {
+                            float a = q == 0 ? af[fm].x : q == 1 ? af[fm].y
+                                                        : q == 2 ? af[fm].z : af[fm].w;
+                            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                a, bf[fn][q], acc[fm][fn], 0, 0, 0);
+                        }
+            }
+            if (kt + 1 < ntk) {
+                store_a(buf ^ 1);
+                store_b(buf ^ 1);
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue.  Accumulator register r of a 32x32 block holds
+    // row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
+    const int nbatch = gridDim.z;
+    const int hw = p.coh * p.cow;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            const int col = n0 + bcol + fn * 32;
+            if (col >= p.N) continue;
+            float bval = (p.splits <= 1 && p.bias) ? p.bias[col] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * (BM / WM) + fm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row >= p.M) continue;
+                float v = acc[fm][fn][r];
+                if (p.splits > 1) {
+                    p.partial[(((int64_t)split * nbatch + bz) * p.M + row) * p.N + col] = v;
+                    continue;
+                }
+                int64_t ci;
+                if constexpr (CM == shp::C_NCHW) {
+                    int img = row / hw, pix = row % hw;
+                    ci = ((int64_t)img * p.N + col) * hw + pix;
+                } else {
+                    ci = bo * p.sc_outer + bi * p.sc_inner + (int64_t)row * p.scm +
+                         (int64_t)col * p.scn;
+                }
+                v += bval;
+                if (p.residual) v += p.residual[ci];
+                p.c[ci] = shpd::apply_act(v, p.act, p.alpha);
+            }
+        }
+}
+
+// Split-K second pass: sum the partials in split order, then the epilogue.
+template <int CM>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int nbatch) {
+    const int64_t mn = (int64_t)p.M * p.N;
+    const int64_t total = mn * nbatch;
+    const int hw = p.coh * p.cow;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        int bz = (int)(i / mn);
+        int64_t rem = i % mn;
+        int row = (int)(rem / p.N), col = (int)(rem % p.N);
+        float v = 0.0f;
+        for (int s = 0; s < p.splits; ++s) v += p.partial[((int64_t)s * nbatch + bz) * mn + rem];
+        int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
+        int64_t ci;
+        if constexpr (CM == shp::C_NCHW) {
+            int img = row / hw, pix = row % hw;
+            ci = ((int64_t)img * p.N + col) * hw + pix;
+        } else {
+            ci = bo * p.sc_outer + bi * p.sc_inner + (int64_t)row * p.scm + (int64_t)col * p.scn;
+        }
+        if (p.bias) v += p.bias[col];
+        if (p.residual) v += p.residual[ci];
+        p.c[ci] = shpd::apply_act(v, p.act, p.alpha);
+    }
+}
+
+// ---- skinny products: M <= 8 rows against a [N][K] weight (fully_connected at batch
+// 1..8).  One wavefront per output column reads that column's K weights once with 16-byte
+// loads; the M activation rows come from cache.  HBM-bound like a GEMV.
+template <int MR>
+__global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        float* __restrict__ y, int M, int N,
+                                                        int K, const float* __restrict__ bias,
+                                                        int act, float alpha) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const float* wr = w + (int64_t)n * K;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    const bool vec = (K % 4 == 0) && (((uintptr_t)w & 15) == 0) && (((uintptr_t)x & 15) == 0);
+    if (vec) {
+        for (int k = lane * 4; k < K; k += 256) {
+            float4 wv = *reinterpret_cast<const float4*>(wr + k);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m < M) {
+                    float4 xv = *reinterpret_cast<const float4*>(x + (int64_t)m * K + k);
+                    acc[m] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+                }
+            }
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) {
+            float wv = wr[k];
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < M) acc[m] += wv * x[(int64_t)m * K + k];
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float v = acc[m];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        acc[m] = v;
+    }
+    if (lane == 0) {
+        float b = bias ? bias[n] : 0.0f;
+        for (int m = 0; m < M; ++m) y[(int64_t)m * N + n] = shpd::apply_act(acc[m] + b, act, alpha);
+    }
+}
+
+// ---- host-side dispatch --------------------------------------------------------------
+struct TileCfg {
+    int bm, bn;
+};
+
+template <int BM, int BN, int WM, int WN, int AM, int BMD, int CM>
+void launch_tile(hipStream_t s, const GemmParams& p, dim3 grid) {
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, AM, BMD, CM>), grid, dim3(256), 0, s, p);
+}
+
+template <int AM, int BMD, int CM>
+void launch_combo(hipStream_t s, const GemmParams& p, TileCfg t, dim3 grid) {
+    if (t.bm == 128 && t.bn == 128)
+        launch_tile<128, 128, 2, 2, AM, BMD, CM>(s, p, grid);
+    else if (t.bm == 128 && t.bn == 64)
+        launch_tile<128, 64, 2, 2, AM, BMD, CM>(s, p, grid);
+    else
+        launch_tile<64, 64, 2, 2, AM, BMD, CM>(s, p, grid);
+}
+
+int dispatch_combo(hipStream_t s, const GemmParams& p, int am, int bm, int cm, TileCfg t,
+                   dim3 grid) {
+    using namespace shp;
+#define SHP_COMBO(A_, B_, C_)                       \
+    if (am == A_ && bm == B_ && cm == C_) {          \
+        launch_combo<A_, B_, C_>(s, p, t, grid);    \
+        return SHP_OK;                              \
+    }
+    SHP_COMBO(A_CONV_NHWC4, B_NVEC, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC4, B_KVEC, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC4, B_STRIDED, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC, B_NVEC, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC, B_KVEC, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC, B_STRIDED, C_STRIDED)
+    SHP_COMBO(A_CONV_NCHW, B_KVEC, C_NCHW)
+    SHP_COMBO(A_CONV_NCHW, B_STRIDED, C_NCHW)
+    SHP_COMBO(A_KVEC, B_NVEC, C_STRIDED)
+    SHP_COMBO(A_KVEC, B_KVEC, C_STRIDED)
+    SHP_COMBO(A_KVEC, B_STRIDED, C_STRIDED)
+    SHP_COMBO(A_STRIDED, B_NVEC, C_STRIDED)
+    SHP_COMBO(A_STRIDED, B_KVEC, C_STRIDED)
+    SHP_COMBO(A_STRIDED, B_STRIDED, C_STRIDED)
+#undef SHP_COMBO
+    return fail(SHP_ERR_UNSUPPORTED, "gemm: unsupported operand mode combination");
+}
+
+TileCfg pick_tile(const GemmParams& p) {
+    int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
+    if (p.N <= 64) return {128, 64};
+    if (t128 >= 256 || p.M > 4096) return {128, 128};
+    return {64, 64};
+}
+
+struct SplitPlan {
+    int splits, kps;
+};
+
+SplitPlan plan_split(const GemmParams& p, TileCfg t, int nbatch) {
+    int64_t tiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * nbatch;
+    SplitPlan sp{1, ((p.K + BK - 1) / BK) * BK};
+    if (tiles >= 192 || p.K < 512) return sp;
+    int want = (int)((512 + tiles - 1) / tiles);
+    int maxs = p.K / 256;
+    if (want > maxs) want = maxs;
+    if (want > 16) want = 16;
+    if (want < 2) return sp;
+    int kps = (p.K + want - 1) / want;
+    kps = ((kps + BK - 1) / BK) * BK;
+    sp.kps = kps;
+    sp.splits = (p.K + kps - 1) / kps;
+    return sp;
+}
+
+}  // namespace
+
+namespace shp {
+
+size_t gemm_workspace_bytes(const GemmParams& p, int, int, int) {
+    TileCfg t = pick_tile(p);
+    int nbatch = p.batch_outer * p.batch_inner;
+    SplitPlan sp = plan_split(p, t, nbatch);
+    if (sp.splits <= 1) return 0;
+    return (size_t)sp.splits * nbatch * p.M * p.N * sizeof(float);
+}
+
+int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
+                float* workspace, size_t workspace_bytes) {
+    if (p.M <= 0 || p.N <= 0 || p.K < 0)
+        return fail(SHP_ERR_SHAPE, "gemm: M, N must be > 0 and K >= 0");
+    int nbatch = p.batch_outer * p.batch_inner;
+    if (nbatch <= 0 || nbatch > 65535) return fail(SHP_ERR_SHAPE, "gemm: batch out of range");
+    if (amode == A_CONV_NHWC4 && p.cic % 4 != 0) amode = A_CONV_NHWC;
+    TileCfg t = pick_tile(p);
+    SplitPlan sp = plan_split(p, t, nbatch);
+    size_t need = sp.splits > 1 ? (size_t)sp.splits * nbatch * p.M * p.N * sizeof(float) : 0;
+    if (sp.splits > 1 && (workspace == nullptr || workspace_bytes < need))
+        sp = SplitPlan{1, ((p.K + BK - 1) / BK) * BK};
+    p.splits = sp.splits;
+    p.k_per_split = sp.kps > 0 ? sp.kps : BK;
+    p.partial = sp.splits > 1 ? workspace : nullptr;
+    int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
+    if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
+    dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
+    int rc = dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
+    if (rc) return rc;
+    SHP_HIP_CHECK(hipGetLastError());
+    if (p.splits > 1) {
+        int64_t total = (int64_t)p.M * p.N * nbatch;
+        unsigned g = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+        if (cmode == C_NCHW)
+            hipLaunchKernelGGL((splitk_reduce_kernel<C_NCHW>), dim3(g), dim3(256), 0, stream, p,
+                               nbatch);
+        else
+            hipLaunchKernelGGL((splitk_reduce_kernel<C_STRIDED>), dim3(g), dim3(256), 0, stream,
+                               p, nbatch);
+        SHP_HIP_CHECK(hipGetLastError());
+    }
+    return SHP_OK;
+}
+
+}  // namespace shp
+
+namespace {
+
+using shp::fail;
+
+inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+GemmParams base_params() {
+    GemmParams p;
+    memset(&p, 0, sizeof(p));
+    p.batch_outer = p.batch_inner = 1;
+    p.coh = p.cow = 1;
+    p.splits = 1;
+    return p;
+}
+
+// hlo_conv_nhwc_hwio: push {n, ih, iw, ic, kh, kw, oc, oh, ow, sh, sw, pt, pl, total}
+int launch_hlo_conv(const shp::Launch& l) {
+    if (l.n_push < 14) return fail(SHP_ERR_PUSH, "hlo_conv_nhwc_hwio needs 14 push constants");
+    const int32_t* q = l.push;
+    for (int i = 0; i < 11; ++i)
+        if (q[i] <= 0) return fail(SHP_ERR_SHAPE, "hlo_conv_nhwc_hwio: non-positive dim/stride");
+    int rc = shp::check_total(l, (int64_t)q[0] * q[7] * q[8] * q[6], "hlo_conv_nhwc_hwio");
+    if (rc) return rc;
+    if (q[13] != (int64_t)q[0] * q[7] * q[8] * q[6])
+        return fail(SHP_ERR_SHAPE, "hlo_conv_nhwc_hwio: total != n*oh*ow*oc");
+    GemmParams p = base_params();
+    p.cn = q[0]; p.cih = q[1]; p.ciw = q[2]; p.cic = q[3]; p.ckh = q[4]; p.ckw = q[5];
+    p.coh = q[7]; p.cow = q[8]; p.csh = q[9]; p.csw = q[10]; p.cpt = q[11]; p.cpl = q[12];
+    p.M = q[0] * q[7] * q[8];
+    p.N = q[6];
+    p.K = q[4] * q[5] * q[3];
+    p.a = (const float*)l.in0;
+    p.b = (const float*)l.in1;
+    p.sbk = p.N;
+    p.sbn = 1;
+    p.c = (float*)l.out;
+    p.scm = p.N;
+    p.scn = 1;
+    p.bias = l.epi->bias;
+    p.residual = l.epi->residual;
+    p.act = l.epi->act;
+    p.alpha = l.epi->alpha;
+    int am = (p.cic % 4 == 0 && al16(p.a)) ? shp::A_CONV_NHWC4 : shp::A_CONV_NHWC;
+    int bm = (p.N % 4 == 0 && al16(p.b)) ? shp::B_NVEC : shp::B_STRIDED;
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+}
+
+// conv2d (NCHW, weights OIHW followed by the bias tail):
+// push {n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, same, pt, pl, total}
+int conv2d_common(const shp::Launch& l, bool nhwc) {
+    if (l.n_push < 15) return fail(SHP_ERR_PUSH, "conv2d needs 15 push constants");
+    const int32_t* q = l.push;
+    for (int i = 0; i < 11; ++i)
+        if (q[i] <= 0) return fail(SHP_ERR_SHAPE, "conv2d: non-positive dim/stride");
+    int64_t total = (int64_t)q[0] * q[4] * q[5] * q[6];
+    int rc = shp::check_total(l, total, "conv2d");
+    if (rc) return rc;
+    if (q[14] != total) return fail(SHP_ERR_SHAPE, "conv2d: total != n*oc*oh*ow");
+    GemmParams p = base_params();
+    p.cn = q[0]; p.cic = q[1]; p.cih = q[2]; p.ciw = q[3];
+    p.coh = q[5]; p.cow = q[6]; p.ckh = q[7]; p.ckw = q[8];
+    p.csh = q[9]; p.csw = q[10]; p.cpt = q[12]; p.cpl = q[13];
+    p.M = q[0] * q[5] * q[6];
+    p.N = q[4];
+    p.K = q[1] * q[7] * q[8];
+    p.a = (const float*)l.in0;
+    p.b = (const float*)l.in1;
+    p.sbk = 1;
+    p.sbn = p.K;
+    p.c = (float*)l.out;
+    p.scm = p.N;
+    p.scn = 1;
+    p.bias = p.b + (int64_t)p.N * p.K;  // packed bias tail (scheduler.rs:1327-1362)
+    p.residual = l.epi->residual;
+    p.act = l.epi->act;
+    p.alpha = l.epi->alpha;
+    int bm = (p.K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
+    if (nhwc) {
+        int am = (p.cic % 4 == 0 && al16(p.a)) ? shp::A_CONV_NHWC4 : shp::A_CONV_NHWC;
+        return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace,
+                                l.workspace_bytes);
+    }
+    return shp::gemm_launch(l.stream, p, shp::A_CONV_NCHW, bm, shp::C_NCHW, l.workspace,
+                            l.workspace_bytes);
+}
+
+int launch_conv2d(const shp::Launch& l) { return conv2d_common(l, false); }
+// conv2d_nhwc (native): the TFLite Conv2D on NHWC activations with the model's own OHWI
+// weights + bias tail — no NCHW relabelling (scheduler.rs:58-62) and no OIHW repack.
+int launch_conv2d_nhwc(const shp::Launch& l) { return conv2d_common(l, true); }
+
+// fully_connected: push {batches, input_size, output_size, total}; weights [out][in] + bias
+int launch_fully_connected(const shp::Launch& l) {
+    if (l.n_push < 4) return fail(SHP_ERR_PUSH, "fully_connected needs 4 push constants");
+    const int32_t* q = l.push;
+    if (q[0] <= 0 || q[1] <= 0 || q[2] <= 0) return fail(SHP_ERR_SHAPE, "fully_connected: dims");
+    int rc = shp::check_total(l, (int64_t)q[0] * q[2], "fully_connected");
+    if (rc) return rc;
+    if (q[3] != (int64_t)q[0] * q[2]) return fail(SHP_ERR_SHAPE, "fully_connected: total");
+    int M = q[0], K = q[1], N = q[2];
+    const float* w = (const float*)l.in1;
+    const float* bias = w + (int64_t)N * K;
+    if (M <= 8 && !l.epi->residual) {
+        unsigned g = (unsigned)((N + 3) / 4);
+        if (M <= 1)
+            hipLaunchKernelGGL((skinny_nt_kernel<1>), dim3(g), dim3(256), 0, l.stream,
+                               (const float*)l.in0, w, (float*)l.out, M, N, K, bias,
+                               l.epi->act, l.epi->alpha);
+        else
+            hipLaunchKernelGGL((skinny_nt_kernel<8>), dim3(g), dim3(256), 0, l.stream,
+                               (const float*)l.in0, w, (float*)l.out, M, N, K, bias,
+                               l.epi->act, l.epi->alpha);
+        SHP_HIP_CHECK(hipGetLastError());
+        return SHP_OK;
+    }
+    GemmParams p = base_params();
+    p.M = M; p.N = N; p.K = K;
+    p.a = (const float*)l.in0; p.sam = K; p.sak = 1;
+    p.b = w; p.sbk = 1; p.sbn = K;
+    p.c = (float*)l.out; p.scm = N; p.scn = 1;
+    p.bias = bias;
+    p.residual = l.epi->residual;
+    p.act = l.epi->act;
+    p.alpha = l.epi->alpha;
+    int am = (K % 4 == 0 && al16(p.a)) ? shp::A_KVEC : shp::A_STRIDED;
+    int bm = (K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+}
+
+// Pick vector modes for a strided batched product when the layout allows them.
+int dot_modes(const GemmParams& p, int& am, int& bm) {
+    bool a4 = p.sak == 1 && p.K % 4 == 0 && p.sam % 4 == 0 && p.sa_outer % 4 == 0 &&
+              p.sa_inner % 4 == 0 && al16(p.a);
+    am = a4 ? shp::A_KVEC : shp::A_STRIDED;
+    bool bn4 = p.sbn == 1 && p.N % 4 == 0 && p.sbk % 4 == 0 && p.sb_outer % 4 == 0 &&
+               p.sb_inner % 4 == 0 && al16(p.b);
+    bool bk4 = p.sbk == 1 && p.K % 4 == 0 && p.sbn % 4 == 0 && p.sb_outer % 4 == 0 &&
+               p.sb_inner % 4 == 0 && al16(p.b);
+    bm = bn4 ? shp::B_NVEC : bk4 ? shp::B_KVEC : shp::B_STRIDED;
+    return SHP_OK;
+}
+
+void dot_epilogue(GemmParams& p, const shp::Launch& l) {
+    p.bias = l.epi->bias;
+    p.residual = l.epi->residual;
+    p.act = l.epi->act;
+    p.alpha = l.epi->alpha;
+}
+
+// hlo_dot_batched: push {batch, m, k, n, total}; lhs [B,M,K], rhs [B,K,N], out [B,M,N]
+int launch_dot_batched(const shp::Launch& l) {
+    if (l.n_push < 5) return fail(SHP_ERR_PUSH, "hlo_dot_batched needs 5 push constants");
+    const int32_t* q = l.push;
+    if (q[0] <= 0 || q[1] <= 0 || q[2] < 0 || q[3] <= 0)
+        return fail(SHP_ERR_SHAPE, "hlo_dot_batched: dims");
+    int64_t total = (int64_t)q[0] * q[1] * q[3];
+    int rc = shp::check_total(l, total, "hlo_dot_batched");
+    if (rc) return rc;
+    if (q[4] != total) return fail(SHP_ERR_SHAPE, "hlo_dot_batched: total");
+    GemmParams p = base_params();
+    p.batch_outer = q[0];
+    p.M = q[1]; p.K = q[2]; p.N = q[3];
+    p.a = (const float*)l.in0; p.sa_outer = (int64_t)p.M * p.K; p.sam = p.K; p.sak = 1;
+    p.b = (const float*)l.in1; p.sb_outer = (int64_t)p.K * p.N; p.sbk = p.N; p.sbn = 1;
+    p.c = (float*)l.out; p.sc_outer = (int64_t)p.M * p.N; p.scm = p.N; p.scn = 1;
+    dot_epilogue(p, l);
+    int am, bm;
+    dot_modes(p, am, bm);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+}
+
+// hlo_dot_rank2: push {m, k, n, total}
+int launch_dot_rank2(const shp::Launch& l) {
+    if (l.n_push < 4) return fail(SHP_ERR_PUSH, "hlo_dot_rank2 needs 4 push constants");
+    const int32_t* q = l.push;
+    if (q[0] <= 0 || q[1] < 0 || q[2] <= 0) return fail(SHP_ERR_SHAPE, "hlo_dot_rank2: dims");
+    int64_t total = (int64_t)q[0] * q[2];
+    int rc = shp::check_total(l, total, "hlo_dot_rank2");
+    if (rc) return rc;
+    if (q[3] != total) return fail(SHP_ERR_SHAPE, "hlo_dot_rank2: total");
+    GemmParams p = base_params();
+    p.M = q[0]; p.K = q[1]; p.N = q[2];
+    p.a = (const float*)l.in0; p.sam = p.K; p.sak = 1;
+    p.b = (const float*)l.in1; p.sbk = p.N; p.sbn = 1;
+    p.c = (float*)l.out; p.scm = p.N; p.scn = 1;
+    dot_epilogue(p, l);
+    int am, bm;
+    dot_modes(p, am, bm);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+}
+
+// dot_general_strided (native): any dot_general with one contracting dim, read in place.
+// push {batch_outer, batch_inner, M, N, K, sa_outer, sa_inner, sam, sak, sb_outer,
+//       sb_inner, sbk, sbn, sc_outer, sc_inner, scm, scn}  (element strides)
+int launch_dot_general(const shp::Launch& l) {
+    if (l.n_push < 17) return fail(SHP_ERR_PUSH, "dot_general_strided needs 17 push constants");
+    const int32_t* q = l.push;
+    if (q[0] <= 0 || q[1] <= 0 || q[2] <= 0 || q[3] <= 0 || q[4] < 0)
+        return fail(SHP_ERR_SHAPE, "dot_general_strided: dims");
+    for (int i = 5; i < 17; ++i)
+        if (q[i] < 0) return fail(SHP_ERR_SHAPE, "dot_general_strided: negative stride");
+    int64_t total = (int64_t)q[0] * q[1] * q[2] * q[3];
+    int rc = shp::check_total(l, total, "dot_general_strided");
+    if (rc) return rc;
+    GemmParams p = base_params();
+    p.batch_outer = q[0]; p.batch_inner = q[1];
+    p.M = q[2]; p.N = q[3]; p.K = q[4];
+    p.a = (const float*)l.in0; p.sa_outer = q[5]; p.sa_inner = q[6]; p.sam = q[7]; p.sak = q[8];
+    p.b = (const float*)l.in1; p.sb_outer = q[9]; p.sb_inner = q[10]; p.sbk = q[11]; p.sbn = q[12];
+    p.c = (float*)l.out; p.sc_outer = q[13]; p.sc_inner = q[14]; p.scm = q[15]; p.scn = q[16];
+    dot_epilogue(p, l);
+    int am, bm;
+    dot_modes(p, am, bm);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+}
+
+}  // namespace
+
+namespace shp {
+
+KernelEntry kGemmKernels[] = {
+    {"hlo_conv_nhwc_hwio", 14, true, launch_hlo_conv},
+    {"conv2d", 15, true, launch_conv2d},
+    {"fully_connected", 4, true, launch_fully_connected},
+    {"hlo_dot_batched", 5, true, launch_dot_batched},
+    {"hlo_dot_rank2", 4, true, launch_dot_rank2},
+    // native extensions
+    {"conv2d_nhwc", 15, true, launch_conv2d_nhwc},
+    {"dot_general_strided", 17, true, launch_dot_general},
+};
+const int kGemmKernelCount = sizeof(kGemmKernels) / sizeof(kGemmKernels[0]);
+
+}  // namespace shp

@@ -1,0 +1,38 @@
+// The context behind shp_ctx: one device, one stream, a split-K workspace and the
+// per-launch event timers that replace KernelOutput.elapsed_ms (vulkan.rs:163-171).
+#pragma once
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace shp {
+
+struct Ctx {
+    int device = -1;
+    int cu_count = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    shp_run_info info{};
+    float* workspace = nullptr;
+    size_t workspace_bytes = 0;
+
+    struct Timer {
+        hipEvent_t a, b;
+        std::string name;
+    };
+    bool timing = false;
+    std::vector<Timer> timers;
+    size_t timer_used = 0;
+    std::map<std::string, std::pair<double, uint64_t>> timing_totals;
+
+    ~Ctx();
+    int ensure_workspace(size_t bytes);
+    int launch(const char* name, const void* in0, const void* in1, void* out,
+               const int32_t* push, size_t n_push, uint64_t out_elems, const shp_epilogue* epi);
+    int collect_timing();
+};
+
+}  // namespace shp

@@ -1,0 +1,371 @@
+"""HIP kernels vs the CPU oracle, through the C ABI, on seeded inputs (GPU).
+
+Gate: per-op |hip - oracle| <= 1e-4 + 1e-4*|oracle| in fp32;
+data movement (copy/transpose/pad/concat) and max-reductions bit-exact.  The reference's
+golden vectors go through the host-to-host drop-in (shp_run_kernel) with the reference's
+own thresholds (tests/parity_test/generate_fixtures.py:108-113).
+"""
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, assert_close, raw_f32, ulp_diff
+
+pytestmark = pytest.mark.gpu
+PARITY = GOLDEN / "parity"
+RNG = np.random.default_rng(20261201)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def f32bits(v):
+    return int(np.array([v], np.float32).view(np.int32)[0])
+
+
+def hip(ctx, name, in0, in1, n_out, push, bias=None, residual=None, act=0, alpha=0.0,
+        out_dtype=np.float32):
+    t0 = ctx.tensor(in0) if in0 is not None else ctx.tensor(np.zeros(1, np.float32))
+    t1 = ctx.tensor(in1) if in1 is not None else ctx.tensor(np.zeros(1, np.float32))
+    tb = ctx.tensor(bias) if bias is not None else None
+    tr = ctx.tensor(residual) if residual is not None else None
+    out = ctx.empty(n_out, out_dtype)
+    print(f"[gpu] {name} push={list(push)[:16]} n_out={n_out}", flush=True)
+    ctx.launch(name, t0, t1, out, push, bias=tb, residual=tr, act=act, alpha=alpha)
+    ctx.sync()
+    y = out.download()
+    for t in (t0, t1, tb, tr, out):
+        if t is not None:
+            t.free()
+    return y
+
+
+def both(ctx, orc, name, in0, in1, n_out, push, **kw):
+    return hip(ctx, name, in0, in1, n_out, push, **kw), orc.run(name, in0, in1, n_out, push, **kw)
+
+
+# ---- golden vectors through the drop-in host-to-host entry -------------------------------
+def test_golden_relu_bit_exact(ctx):
+    from spirv_inference_amd import KernelRun
+    x = raw_f32(PARITY / "relu_input.raw.f32")
+    out = ctx.run_kernel(KernelRun("relu", "relu", x, np.zeros(1, np.float32), x.size,
+                                   (x.size + 127) // 128, [x.size]))
+    assert out.vendor_id == 0x1002
+    assert out.values.tobytes() == raw_f32(PARITY / "relu_ref.raw.f32").tobytes()
+
+
+def test_golden_softmax(ctx):
+    from spirv_inference_amd import KernelRun
+    x = raw_f32(PARITY / "softmax_input.raw.f32")
+    out = ctx.run_kernel(KernelRun("softmax", "softmax1000", x, np.zeros(1, np.float32), 128, 1,
+                                   [128]))
+    ref = raw_f32(PARITY / "softmax_ref.raw.f32")
+    assert ulp_diff(out.values, ref).max() <= 8 and np.abs(out.values - ref).max() <= 1e-6
+
+
+def test_golden_conv1d(ctx):
+    from spirv_inference_amd import KernelRun
+    x = raw_f32(PARITY / "conv1d_input.raw.f32")
+    w = raw_f32(PARITY / "conv1d_filter.raw.f32")
+    push = [1, 16, 1, 64, 3, 1, 32, 16, 1, 1, 1, 1, 0, 512]
+    out = ctx.run_kernel(KernelRun("conv1d", "hlo_conv_nhwc_hwio", x, w, 512, 8, push))
+    ref = raw_f32(PARITY / "conv1d_ref.raw.f32")
+    rel = np.abs(out.values - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert ulp_diff(out.values, ref).max() <= 16 or rel.max() <= 1e-5
+
+
+def test_golden_batchnorm(ctx, orc):
+    from spirv_inference_amd import KernelRun
+    x = raw_f32(PARITY / "batchnorm_input.raw.f32")
+    mean, var, gamma, beta, eps = raw_f32(PARITY / "batchnorm_params.raw.f32")
+    n = x.size
+    full = lambda v: np.full(n, v, np.float32)
+    run = lambda k, a, b: ctx.run_kernel(KernelRun(k, k, a, b, n, 2, [n])).values
+    inv = run("rsqrt", run("add", full(var), full(eps)), np.zeros(1, np.float32))
+    y = run("add", run("mul", run("mul", run("sub", x, full(mean)), inv), full(gamma)),
+            full(beta))
+    ref = raw_f32(PARITY / "batchnorm_ref.raw.f32")
+    assert ulp_diff(y, ref).max() <= 8 and np.abs(y - ref).max() <= 1e-6
+
+
+# ---- elementwise ---------------------------------------------------------------------------
+UNARY = ["abs", "exp", "log", "neg", "sqrt", "rsqrt", "sigmoid", "logistic", "tanh", "relu",
+         "relu6", "sine", "reshape", "silu", "gelu_erf", "cosine", "floor", "ceil"]
+
+
+@pytest.mark.parametrize("name", UNARY)
+@pytest.mark.parametrize("n", [1, 7, 4099, 1 << 20])
+def test_unary(ctx, orc, name, n):
+    x = rnd(n, scale=3.0)
+    if name in ("log", "sqrt", "rsqrt"):
+        x = np.abs(x) + 0.01
+    y, r = both(ctx, orc, name, x, None, n, [n])
+    if name in ("reshape", "abs", "neg", "relu", "relu6", "floor", "ceil"):
+        assert y.tobytes() == r.tobytes()
+    else:
+        assert_close(y, r, 1e-4, 1e-4, name)
+
+
+def test_leaky_relu(ctx, orc):
+    x = rnd(1000)
+    y, r = both(ctx, orc, "leaky_relu", x, None, 1000, [1000, f32bits(0.2)])
+    assert y.tobytes() == r.tobytes()
+
+
+@pytest.mark.parametrize("name", ["add", "sub", "mul", "div", "pow", "min", "max"])
+@pytest.mark.parametrize("n", [5, 65537])
+def test_binary(ctx, orc, name, n):
+    a, b = rnd(n), rnd(n)
+    if name == "pow":
+        a = np.abs(a) + 0.1
+    if name == "div":
+        b = np.where(np.abs(b) < 0.1, 0.5, b).astype(np.float32)
+    y, r = both(ctx, orc, name, a, b, n, [n])
+    if name in ("add", "sub", "mul", "div", "min", "max"):
+        assert y.tobytes() == r.tobytes()
+    else:
+        assert_close(y, r, 1e-4, 1e-4, name)
+
+
+def test_data_movement_bit_exact(ctx, orc):
+    a, b = rnd(1000), rnd(37)
+    y, r = both(ctx, orc, "concat", a, b, 1037, [1000, 1037])
+    assert y.tobytes() == r.tobytes()
+    x = rnd(2, 5, 6, 7)
+    for perm in [(0, 2, 3, 1), (0, 3, 1, 2), (0, 1, 3, 2), (1, 0, 2, 3), (3, 1, 2, 0)]:
+        out_shape = [x.shape[p] for p in perm]
+        push = [*x.shape, *out_shape, *perm, x.size]
+        y, r = both(ctx, orc, "transpose", x, None, x.size, push)
+        assert y.tobytes() == r.tobytes(), perm
+    big = rnd(32, 112, 112, 64)[:1]  # NHWC -> NCHW at a ResNet stage-1 shape
+    push = [1, 112, 112, 64, 1, 64, 112, 112, 0, 3, 1, 2, big.size]
+    y, r = both(ctx, orc, "transpose", big, None, big.size, push)
+    assert y.tobytes() == r.tobytes()
+    push = [32, 230, 230, 3, 32, 224, 224, 3, 0, 3, 3, 0, 32 * 230 * 230 * 3]
+    x = rnd(32, 224, 224, 3)
+    y, r = both(ctx, orc, "pad", x, np.array([0.0], np.float32), push[12], push)
+    assert y.tobytes() == r.tobytes()
+
+
+def test_l2_and_broadcast(ctx, orc):
+    x = rnd(5000)
+    y, r = both(ctx, orc, "l2_normalization", x, None, 5000, [5000])
+    assert_close(y, r, 1e-6, 1e-4, "l2_normalization")
+    nb = f32bits(float(np.linalg.norm(x)))
+    y, r = both(ctx, orc, "l2norm", x, None, 5000, [5000, nb])
+    assert y.tobytes() == r.tobytes()
+    a, b = rnd(3, 1, 4), rnd(1, 5, 4)
+    for op in range(7):
+        aa = np.abs(a) + 0.1 if op == 4 else a
+        push = [op, 60, 1, 3, 5, 4, 0, 4, 0, 1, 0, 0, 4, 1]
+        y, r = both(ctx, orc, "broadcast_binary", aa, b, 60, push)
+        assert_close(y, r, 1e-5, 1e-5, f"broadcast op {op}")
+
+
+def test_bias_act(ctx, orc):
+    x, b, res = rnd(4, 100), rnd(100), rnd(4, 100)
+    for act in range(8):
+        y, r = both(ctx, orc, "bias_act", x, None, 400, [400, 100], bias=b, residual=res, act=act,
+                    alpha=0.1)
+        assert_close(y, r, 1e-5, 1e-5, f"bias_act {act}")
+
+
+# ---- reductions / pools / softmax / norms ------------------------------------------------
+def test_reduce_rank4(ctx, orc):
+    x = rnd(8, 12, 128, 128)
+    for axes in [(3,), (1, 2), (0,), (2,), (0, 1, 2, 3)]:
+        flags = [1 if a in axes else 0 for a in range(4)]
+        od = [1 if f else d for d, f in zip(x.shape, flags)]
+        n_out = int(np.prod([d for d, f in zip(x.shape, flags) if not f]))
+        for kind in (0, 1):
+            push = [4, *x.shape, *od, *flags, kind, n_out]
+            y, r = both(ctx, orc, "hlo_reduce_rank4", x, None, n_out, push)
+            if kind == 1:
+                assert y.tobytes() == r.tobytes()
+            else:
+                assert_close(y, r, 1e-4, 1e-4, f"reduce sum {axes}")
+
+
+def test_resnet_pools(ctx, orc):
+    x = np.abs(rnd(32, 112, 112, 64))
+    # maxpool 3x3 s2 over the padded [32,114,114,64] (resnet50.stablehlo.txt:64-66)
+    push = [32, 112, 112, 64, 56, 56, 3, 3, 2, 2, 1, 1, 1, 32 * 56 * 56 * 64]
+    y, r = both(ctx, orc, "hlo_reduce_window_rank4", x, None, push[13], push)
+    assert y.tobytes() == r.tobytes()
+    x = rnd(2, 16, 21, 21)
+    push = [2, 16, 21, 21, 11, 11, 3, 3, 2, 2, 1, 1, 1, 2 * 16 * 11 * 11]
+    y, r = both(ctx, orc, "max_pool2d", x, None, push[13], push)
+    assert y.tobytes() == r.tobytes()
+    x = rnd(32, 7, 7, 2048)
+    y, r = both(ctx, orc, "global_avg_pool_nhwc", x, None, 32 * 2048, [32, 7, 7, 2048])
+    assert_close(y, r, 1e-5, 1e-4, "gap nhwc")
+    xc = rnd(8, 1280, 7, 7)
+    y, r = both(ctx, orc, "global_avg_pool_sum", xc, None, 8 * 1280, [8, 1280, 7, 7])
+    assert_close(y, r, 1e-4, 1e-4, "gap sum")
+    y2, r2 = both(ctx, orc, "global_avg_pool_finalize", r, None, 8 * 1280, [8, 1280, 7, 7])
+    assert y2.tobytes() == r2.tobytes()
+
+
+def test_softmax_kernels(ctx, orc):
+    x = rnd(10)
+    y, r = both(ctx, orc, "softmax10", x, None, 10, [])
+    assert_close(y, r, 1e-7, 1e-5, "softmax10")
+    x = rnd(8, 1000, scale=4.0)  # EffNet-Lite0 head: whole-tensor semantics at batch 8
+    y, r = both(ctx, orc, "softmax1000", x, None, 8000, [8000])
+    assert_close(y, r, 1e-7, 1e-4, "softmax1000")
+    for rows, cols in [(96 * 128, 128), (3, 32000), (7, 1)]:
+        x = rnd(rows, cols, scale=3.0)
+        mask = rnd(cols)
+        push = [rows, cols, f32bits(0.125)]
+        y, r = both(ctx, orc, "softmax_rows", x, mask, rows * cols, push)
+        assert_close(y, r, 1e-6, 1e-4, f"softmax_rows {rows}x{cols}")
+
+
+def test_row_norms(ctx, orc):
+    x = rnd(1024, 768, scale=2.0)
+    gb = np.concatenate([rnd(768), rnd(768)])
+    push = [1024, 768, f32bits(1e-12)]
+    y, r = both(ctx, orc, "layernorm_rows", x, gb, x.size, push)
+    assert_close(y, r, 1e-4, 1e-4, "layernorm")
+    x = rnd(4, 2048)
+    push = [4, 2048, f32bits(1e-5)]
+    y, r = both(ctx, orc, "rmsnorm_rows", x, np.ones(2048, np.float32), x.size, push)
+    assert_close(y, r, 1e-5, 1e-4, "rmsnorm")
+
+
+# ---- spatial -------------------------------------------------------------------------------
+@pytest.mark.parametrize("k,s,c,n,hw", [(3, 1, 32, 1, 112), (3, 2, 96, 1, 112),
+                                        (5, 2, 144, 8, 56), (5, 1, 1152, 8, 7), (3, 1, 6, 2, 9)])
+def test_depthwise(ctx, orc, k, s, c, n, hw):
+    pt = pl = (k - 1) // 2
+    oh = (hw + 2 * pt - k) // s + 1
+    total = n * c * oh * oh
+    push = [n, c, hw, hw, oh, oh, k, k, s, s, 1, pt, pl, 1, 1, total]
+    x = rnd(n, hw, hw, c)
+    w = np.concatenate([rnd(k * k * c, scale=0.3), rnd(c)])
+    res = rnd(total)
+    y, r = both(ctx, orc, "depthwise_conv2d_nhwc", x, w, total, push, act="relu6")
+    assert_close(y, r, 1e-4, 1e-4, "dw nhwc")
+    y, r = both(ctx, orc, "depthwise_conv2d", x, w, total, push, residual=res)
+    assert_close(y, r, 1e-4, 1e-4, "dw nchw")
+
+
+def test_resize_bilinear(ctx, orc):
+    x = rnd(2, 3, 17, 13)
+    for ac, hp in [(1, 0), (0, 1), (0, 0)]:
+        push = [2, 3, 17, 13, 33, 29, ac, hp, 2 * 3 * 33 * 29]
+        y, r = both(ctx, orc, "resize_bilinear", x, None, push[8], push)
+        assert_close(y, r, 1e-5, 1e-5, f"resize {ac}{hp}")
+
+
+# ---- dense contractions on MFMA -----------------------------------------------------------
+# ResNet-50 v1.5 conv shapes (HLO path, NHWC/HWIO): (ih, ic, k, oc, stride)
+RESNET_CONVS = [(224, 3, 7, 64, 2), (56, 64, 1, 64, 1), (56, 64, 3, 64, 1), (56, 64, 1, 256, 1),
+                (56, 256, 1, 64, 1), (56, 256, 1, 128, 1), (56, 128, 3, 128, 2),
+                (28, 128, 1, 512, 1), (56, 256, 1, 512, 2), (28, 512, 1, 256, 1),
+                (28, 256, 3, 256, 2), (14, 256, 1, 1024, 1), (14, 1024, 1, 512, 1),
+                (14, 512, 3, 512, 2), (7, 512, 1, 2048, 1), (14, 1024, 1, 2048, 2)]
+
+
+@pytest.mark.parametrize("ih,ic,k,oc,s", RESNET_CONVS)
+def test_hlo_conv_resnet_shapes(ctx, orc, ih, ic, k, oc, s):
+    n = 2
+    pad = (k - 1) // 2 if k > 1 else 0
+    oh = (ih + 2 * pad - k) // s + 1
+    x = rnd(n, ih, ih, ic)
+    w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+    b, res = rnd(oc, scale=0.01), rnd(n * oh * oh * oc)
+    push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+    y, r = both(ctx, orc, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res,
+                act="relu")
+    assert_close(y, r, 1e-4, 1e-4, f"conv {ih}x{ic} k{k} oc{oc} s{s}")
+
+
+@pytest.mark.parametrize("ih,ic,k,oc,s", [(7, 512, 3, 512, 1), (56, 64, 3, 64, 1)])
+def test_hlo_conv_full_batch(ctx, orc, ih, ic, k, oc, s):
+    """b32 shapes: the late 3x3 layer exercises split-K, the early one the big tile grid."""
+    n, pad = 32, 1
+    oh = ih
+    x = rnd(n, ih, ih, ic)
+    w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+    push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+    y, r = both(ctx, orc, "hlo_conv_nhwc_hwio", x, w, push[13], push)
+    assert_close(y, r, 1e-4, 1e-4, "conv b32")
+
+
+@pytest.mark.parametrize("n,ic,hw,oc,k,s,pad", [(1, 3, 224, 32, 3, 2, 0), (2, 6, 13, 10, 3, 1, 1),
+                                                (1, 32, 28, 64, 1, 1, 0), (2, 5, 9, 7, 5, 2, 2)])
+def test_conv2d_reference_and_nhwc(ctx, orc, n, ic, hw, oc, k, s, pad):
+    oh = (hw + 2 * pad - k) // s + 1
+    total = n * oc * oh * oh
+    push = [n, ic, hw, hw, oc, oh, oh, k, k, s, s, 1, pad, pad, total]
+    w = np.concatenate([rnd(oc * ic * k * k, scale=0.3), rnd(oc)])
+    x = rnd(n, ic, hw, hw)
+    y, r = both(ctx, orc, "conv2d", x, w, total, push)
+    assert_close(y, r, 1e-4, 1e-4, "conv2d nchw")
+    y, r = both(ctx, orc, "conv2d_nhwc", np.transpose(x, (0, 2, 3, 1)), w, total, push,
+                act="relu6")
+    assert_close(y, r, 1e-4, 1e-4, "conv2d nhwc")
+
+
+@pytest.mark.parametrize("b,k,n", [(1, 1280, 1000), (8, 1280, 1000), (32, 2048, 1000),
+                                   (3, 37, 5)])
+def test_fully_connected(ctx, orc, b, k, n):
+    w = np.concatenate([rnd(n * k, scale=0.05), rnd(n)])
+    x = rnd(b, k)
+    y, r = both(ctx, orc, "fully_connected", x, w, b * n, [b, k, n, b * n])
+    assert_close(y, r, 1e-4, 1e-4, "fc")
+
+
+@pytest.mark.parametrize("bt,m,k,n", [(1, 32, 2048, 1000), (96, 128, 64, 128), (96, 128, 128, 64),
+                                      (1, 1024, 768, 3072), (2, 33, 17, 65), (1, 64, 2048, 256)])
+def test_dot_batched(ctx, orc, bt, m, k, n):
+    a, b = rnd(bt, m, k), rnd(bt, k, n, scale=0.1)
+    y, r = both(ctx, orc, "hlo_dot_batched", a, b, bt * m * n, [bt, m, k, n, bt * m * n])
+    assert_close(y, r, 1e-4, 1e-4, "dot_batched")
+    if bt == 1:
+        y, r = both(ctx, orc, "hlo_dot_rank2", a[0], b[0], m * n, [m, k, n, m * n],
+                    bias=rnd(n), act="gelu_erf")
+        assert_close(y, r, 1e-4, 1e-4, "dot_rank2")
+
+
+def test_dot_general_in_place_attention(ctx, orc):
+    """BERT b8 s128: scores = Q K^T and P V read straight from [B, S, H, D]."""
+    B, S, H, D = 8, 128, 12, 64
+    q, k, v = rnd(B, S, H, D), rnd(B, S, H, D), rnd(B, S, H, D)
+    push = [B, H, S, S, D, S * H * D, D, H * D, 1, S * H * D, D, 1, H * D, H * S * S, S * S, S, 1]
+    y, r = both(ctx, orc, "dot_general_strided", q, k, B * H * S * S, push)
+    assert_close(y, r, 1e-4, 1e-4, "QK^T")
+    p = rnd(B, H, S, S, scale=0.1)
+    push = [B, H, S, D, S, H * S * S, S * S, S, 1, S * H * D, D, H * D, 1, S * H * D, D, H * D, 1]
+    y, r = both(ctx, orc, "dot_general_strided", p, v, B * S * H * D, push)
+    assert_close(y, r, 1e-4, 1e-4, "PV")
+
+
+def test_gemv_and_argmax(ctx, orc):
+    x, w = rnd(2048), rnd(2560, 2048, scale=0.02)
+    y, r = both(ctx, orc, "gemv_nt", x, w, 2560, [2560, 2048])
+    assert_close(y, r, 1e-5, 1e-4, "gemv_nt")
+    res = rnd(2560)
+    y, r = both(ctx, orc, "gemv_nt", x, w, 2560, [2560, 2048], residual=res)
+    assert_close(y, r, 1e-5, 1e-4, "gemv_nt residual")
+    y, r = both(ctx, orc, "gemv_nt", x[:37], rnd(5, 37), 5, [5, 37], bias=rnd(5), act="silu")
+    assert_close(y, r, 1e-5, 1e-4, "gemv_nt generic")
+    logits = rnd(3, 32000)
+    logits[1, 77] = logits[1, 4000] = 99.0  # tie -> lowest index
+    y = hip(ctx, "argmax_rows", logits, None, 3, [3, 32000], out_dtype=np.int32)
+    assert list(y) == [int(np.argmax(l)) for l in logits] and y[1] == 77
+
+
+def test_errors_fail_closed(ctx):
+    from spirv_inference_amd import ShpError
+    t = ctx.tensor(np.zeros(8, np.float32))
+    with pytest.raises(ShpError, match="UNKNOWN_KERNEL"):
+        ctx.launch("no_such_kernel", t, t, t, [8])
+    with pytest.raises(ShpError, match="PUSH"):
+        ctx.launch("conv2d", t, t, t, [1, 2, 3])
+    with pytest.raises(ShpError, match="SHAPE"):
+        ctx.launch("add", t, t, t, [9])
+    with pytest.raises(ShpError, match="UNSUPPORTED"):
+        ctx.launch("add", t, t, t, [8], act="relu")
+    t.free()

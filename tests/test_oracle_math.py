@@ -1,0 +1,227 @@
+"""Pins the oracle kernels that no reference golden vector covers, against independent
+implementations (numpy / torch CPU in float64, closed forms and invariants).  CPU only."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close
+
+RNG = np.random.default_rng(1234)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def conv_nhwc_ref(x, w, stride, pad):
+    """float64 brute force: x [N,H,W,C], w [KH,KW,C,O], pads (top,left) with zero fill."""
+    n, ih, iw, c = x.shape
+    kh, kw, _, o = w.shape
+    sh, sw = stride
+    pt, pl = pad
+    oh = (ih + 2 * pt - kh) // sh + 1
+    ow = (iw + 2 * pl - kw) // sw + 1
+    xp = np.zeros((n, ih + 2 * pt + kh, iw + 2 * pl + kw, c))
+    xp[:, pt:pt + ih, pl:pl + iw] = x
+    out = np.zeros((n, oh, ow, o))
+    for ky in range(kh):
+        for kx in range(kw):
+            patch = xp[:, ky:ky + sh * oh:sh, kx:kx + sw * ow:sw, :]
+            out += np.einsum("nhwc,co->nhwo", patch, w[ky, kx].astype(np.float64))
+    return out
+
+
+@pytest.mark.parametrize("shape", [(2, 9, 11, 5, 3, 3, 7, 1, 1, 1), (1, 16, 16, 8, 3, 3, 12, 2, 1, 1),
+                                   (2, 15, 13, 3, 7, 7, 16, 2, 3, 3), (1, 7, 7, 32, 1, 1, 20, 1, 0, 0)])
+def test_hlo_conv_vs_float64(orc, shape):
+    n, ih, iw, ic, kh, kw, oc, s, pt, pl = shape
+    x, w = rnd(n, ih, iw, ic), rnd(kh, kw, ic, oc, scale=0.2)
+    ref = conv_nhwc_ref(x, w, (s, s), (pt, pl))
+    oh, ow = ref.shape[1:3]
+    push = [n, ih, iw, ic, kh, kw, oc, oh, ow, s, s, pt, pl, ref.size]
+    y = orc.run("hlo_conv_nhwc_hwio", x, w, ref.size, push)
+    assert_close(y, ref, 1e-5, 1e-5, "hlo_conv")
+
+
+def test_conv2d_nchw_and_nhwc_conjugate(orc):
+    n, ic, ih, iw, oc, kh, kw, s = 2, 6, 10, 9, 5, 3, 3, 2
+    pt, pl = orc.same_padding(True, ih, iw, 5, 5, kh, kw, s, s)
+    x = rnd(n, ih, iw, ic)
+    w_ohwi, b = rnd(oc, kh, kw, ic, scale=0.3), rnd(oc)
+    ref = conv_nhwc_ref(x, np.transpose(w_ohwi, (1, 2, 3, 0)), (s, s), (pt, pl))
+    oh, ow = ref.shape[1:3]
+    ref = ref + b
+    total = n * oc * oh * ow
+    push = [n, ic, ih, iw, oc, oh, ow, kh, kw, s, s, 1, pt, pl, total]
+    y = orc.run("conv2d", np.transpose(x, (0, 3, 1, 2)), orc.pack_conv_weight(w_ohwi, b), total,
+                push)
+    assert_close(np.transpose(y.reshape(n, oc, oh, ow), (0, 2, 3, 1)), ref, 1e-5, 1e-5, "conv2d")
+    packed_nhwc = np.concatenate([w_ohwi.reshape(-1), b])
+    y2 = orc.run("conv2d_nhwc", x, packed_nhwc, total, push)
+    assert_close(y2, ref, 1e-5, 1e-5, "conv2d_nhwc")
+
+
+def test_same_padding_matches_tf_rule(orc):
+    # TF SAME: total = max((out-1)*s + k - in, 0); top = total // 2 (scheduler.rs:1597-1614)
+    assert orc.same_padding(True, 224, 224, 112, 112, 3, 3, 2, 2) == (0, 0)
+    assert orc.same_padding(True, 112, 112, 112, 112, 3, 3, 1, 1) == (1, 1)
+    assert orc.same_padding(True, 14, 14, 7, 7, 5, 5, 2, 2) == (1, 1)
+    assert orc.same_padding(False, 14, 14, 7, 7, 5, 5, 2, 2) == (0, 0)
+
+
+@pytest.mark.parametrize("nhwc", [False, True])
+def test_depthwise_vs_float64(orc, nhwc):
+    n, c, ih, iw, k, s, dil = 2, 8, 11, 10, 5, 2, 1
+    pt, pl = 2, 2
+    x = rnd(n, ih, iw, c)
+    w, b = rnd(k, k, c, scale=0.3), rnd(c)
+    oh, ow = (ih + 2 * pt - k) // s + 1, (iw + 2 * pl - k) // s + 1
+    xp = np.zeros((n, ih + 2 * pt + k, iw + 2 * pl + k, c))
+    xp[:, pt:pt + ih, pl:pl + iw] = x
+    ref = np.zeros((n, oh, ow, c)) + b
+    for ky in range(k):
+        for kx in range(k):
+            ref += xp[:, ky:ky + s * oh:s, kx:kx + s * ow:s, :] * w[ky, kx]
+    total = n * c * oh * ow
+    push = [n, c, ih, iw, oh, ow, k, k, s, s, 1, pt, pl, dil, dil, total]
+    if nhwc:
+        y = orc.run("depthwise_conv2d_nhwc", x, np.concatenate([w.reshape(-1), b]), total, push)
+        assert_close(y, ref, 1e-5, 1e-5, "dw nhwc")
+    else:
+        y = orc.run("depthwise_conv2d", np.transpose(x, (0, 3, 1, 2)),
+                    orc.pack_depthwise_weight(w, b), total, push)
+        assert_close(np.transpose(y.reshape(n, c, oh, ow), (0, 2, 3, 1)), ref, 1e-5, 1e-5, "dw")
+
+
+def test_fully_connected_and_dots_vs_matmul(orc):
+    x, w, b = rnd(3, 40), rnd(17, 40), rnd(17)
+    y = orc.run("fully_connected", x, orc.pack_fc_weight(w, b), 51, [3, 40, 17, 51])
+    assert_close(y, x.astype(np.float64) @ w.T.astype(np.float64) + b, 1e-5, 1e-5, "fc")
+    a, bb = rnd(4, 5, 33), rnd(4, 33, 7)
+    y = orc.run("hlo_dot_batched", a, bb, 140, [4, 5, 33, 7, 140])
+    assert_close(y, np.matmul(a.astype(np.float64), bb), 1e-5, 1e-5, "dot_batched")
+    y = orc.run("hlo_dot_rank2", a[0], bb[0], 35, [5, 33, 7, 35])
+    assert_close(y, a[0].astype(np.float64) @ bb[0], 1e-5, 1e-5, "dot_rank2")
+    # dot_general in place: scores = Q K^T for Q,K in [B, S, H, D] (BERT layout)
+    B, S, H, D = 2, 6, 3, 8
+    q, k = rnd(B, S, H, D), rnd(B, S, H, D)
+    push = [B, H, S, S, D, S * H * D, D, H * D, 1, S * H * D, D, 1, H * D, H * S * S, S * S, S, 1]
+    y = orc.run("dot_general_strided", q, k, B * H * S * S, push)
+    ref = np.einsum("bshd,bthd->bhst", q.astype(np.float64), k)
+    assert_close(y, ref, 1e-5, 1e-5, "dot_general")
+
+
+def test_reductions_vs_numpy(orc):
+    x = rnd(3, 4, 5, 6)
+    for axes in [(3,), (1, 2), (0,), (0, 1, 2, 3)]:
+        flags = [1 if a in axes else 0 for a in range(4)]
+        od = [1 if f else d for d, f in zip(x.shape, flags)]
+        for kind, fn in [(0, np.sum), (1, np.max)]:
+            ref = fn(x.astype(np.float64), axis=axes)
+            push = [4, *x.shape, *od, *flags, kind, ref.size]
+            y = orc.run("hlo_reduce_rank4", x, None, ref.size, push)
+            assert_close(y, ref, 1e-5, 1e-5, f"reduce {axes} {kind}")
+
+
+def test_pools_vs_numpy(orc):
+    x = rnd(2, 9, 9, 4)
+    t = torch.from_numpy(np.transpose(x, (0, 3, 1, 2)).astype(np.float64))
+    ref = torch.nn.functional.max_pool2d(t, 3, 2, padding=1).numpy()
+    oh, ow = ref.shape[2:]
+    push = [2, 9, 9, 4, oh, ow, 3, 3, 2, 2, 1, 1, 1, ref.size]
+    y = orc.run("hlo_reduce_window_rank4", x, None, ref.size, push)
+    assert_close(y, np.transpose(ref, (0, 2, 3, 1)), 0, 0, "reduce_window max")
+    push = [2, 4, 9, 9, oh, ow, 3, 3, 2, 2, 1, 1, 1, ref.size]
+    y = orc.run("max_pool2d", np.transpose(x, (0, 3, 1, 2)), None, ref.size, push)
+    assert_close(y, ref, 0, 0, "max_pool2d")
+    s = orc.run("global_avg_pool_sum", np.transpose(x, (0, 3, 1, 2)), None, 8, [2, 4, 9, 9])
+    m = orc.run("global_avg_pool_finalize", s, None, 8, [2, 4, 9, 9])
+    assert_close(m, x.astype(np.float64).mean(axis=(1, 2)), 1e-6, 1e-5, "gap")
+    m2 = orc.run("global_avg_pool_nhwc", x, None, 8, [2, 9, 9, 4])
+    assert_close(m2, x.astype(np.float64).mean(axis=(1, 2)), 1e-6, 1e-5, "gap nhwc")
+
+
+def test_softmax_and_norms_vs_float64(orc):
+    x = rnd(5, 37)
+    mask = rnd(37)
+    scale = np.float32(0.125)
+    ref = torch.softmax(torch.from_numpy(x.astype(np.float64) * scale + mask), -1).numpy()
+    bits = int(np.array([scale], np.float32).view(np.int32)[0])
+    y = orc.run("softmax_rows", x, mask, x.size, [5, 37, bits])
+    assert_close(y, ref, 1e-6, 1e-5, "softmax_rows")
+    assert np.allclose(y.reshape(5, 37).sum(-1), 1.0, atol=1e-6)
+    g, b = rnd(37), rnd(37)
+    eps = np.float32(1e-5)
+    eb = int(np.array([eps], np.float32).view(np.int32)[0])
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float64)), (37,),
+                                         torch.from_numpy(g.astype(np.float64)),
+                                         torch.from_numpy(b.astype(np.float64)), eps=1e-5).numpy()
+    y = orc.run("layernorm_rows", x, np.concatenate([g, b]), x.size, [5, 37, eb])
+    assert_close(y, ref, 1e-5, 1e-5, "layernorm")
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-5) * g
+    y = orc.run("rmsnorm_rows", x, g, x.size, [5, 37, eb])
+    assert_close(y, ref, 1e-5, 1e-5, "rmsnorm")
+
+
+def test_gelu_erfc_expansion_vs_exact(orc):
+    from scipy.special import erfc
+    x = np.linspace(-12, 12, 4001).astype(np.float32)
+    y = orc.run("gelu_erf", x, None, x.size, [x.size])
+    xd = x.astype(np.float64)
+    ref = 0.5 * xd * erfc(-xd / np.sqrt(2.0))
+    assert_close(y, ref, 2e-6, 2e-6, "gelu (XLA erfc expansion)")
+
+
+def test_data_movement_bit_exact(orc):
+    x = rnd(2, 3, 4, 5)
+    for perm in [(0, 2, 3, 1), (0, 3, 1, 2), (1, 0, 3, 2), (3, 2, 1, 0)]:
+        ref = np.transpose(x, perm)
+        push = [*x.shape, *ref.shape, *perm, x.size]
+        y = orc.run("transpose", x, None, x.size, push)
+        assert y.tobytes() == np.ascontiguousarray(ref).tobytes()
+    ref = np.pad(x, [(0, 0), (1, 2), (3, 0), (0, 1)], constant_values=-2.5)
+    push = [*ref.shape, *x.shape, 0, 1, 3, 0, ref.size]
+    y = orc.run("pad", x, np.array([-2.5], np.float32), ref.size, push)
+    # pad.comp only honours low pads; the high side is whatever remains of the output
+    assert y.tobytes() == np.ascontiguousarray(ref).tobytes()
+    a, b = rnd(7), rnd(5)
+    y = orc.run("concat", a, b, 12, [7, 12])
+    assert y.tobytes() == np.concatenate([a, b]).tobytes()
+    y = orc.run("reshape", a, None, 7, [7])
+    assert y.tobytes() == a.tobytes()
+
+
+def test_broadcast_binary_and_l2(orc):
+    a, b = rnd(3, 1, 4), rnd(1, 5, 4)
+    ref = a * b  # float32 product: one rounding, bit-exact
+    push = [2, ref.size, 1, 3, 5, 4, 0, 4, 0, 1, 0, 0, 4, 1]
+    y = orc.run("broadcast_binary", a, b, ref.size, push)
+    assert_close(y, ref, 0, 0, "broadcast mul")
+    x = rnd(100)
+    y = orc.run("l2_normalization", x, None, 100, [100])
+    assert_close(y, x / np.linalg.norm(x.astype(np.float64)), 1e-6, 1e-5, "l2")
+    nb = int(np.array([np.linalg.norm(x)], np.float32).view(np.int32)[0])
+    y = orc.run("l2norm", x, None, 100, [100, nb])
+    assert_close(y, x / np.linalg.norm(x.astype(np.float64)), 1e-6, 1e-5, "l2norm")
+
+
+def test_resize_bilinear_vs_torch(orc):
+    x = rnd(1, 3, 6, 7)
+    for ac, hp in [(1, 0), (0, 1)]:
+        ref = torch.nn.functional.interpolate(torch.from_numpy(x.astype(np.float64)),
+                                              size=(11, 9), mode="bilinear",
+                                              align_corners=bool(ac)).numpy()
+        push = [1, 3, 6, 7, 11, 9, ac, hp, ref.size]
+        y = orc.run("resize_bilinear", x, None, ref.size, push)
+        assert_close(y, ref, 1e-5, 1e-5, f"resize ac={ac} hp={hp}")
+
+
+def test_argmax_tie_rules(orc):
+    v = np.array([1, 5, 2, 5, 0], np.float32)
+    assert orc.argmax_first(v) == 1               # numpy argmax (run_llama_spirv.py:252-254)
+    assert orc.top1_reference(v)[0] == 3          # Rust max_by keeps the last maximum
+    v1001 = np.zeros(1001, np.float32)
+    v1001[0] = 9.0
+    v1001[10] = 3.0
+    assert orc.top1_reference(v1001)[0] == 9      # background class skipped, offset by one
