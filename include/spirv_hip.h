@@ -95,7 +95,8 @@ int shp_sync(shp_ctx* ctx);
 
 /* Deterministic counter-based fill used for the synthetic inputs and random-init
  * weights of the benchmark configs: value i of tensor `tensor_id` depends only on
- * (seed, tensor_id, i).  kind 0: uniform [lo, hi); kind 1: normal(mean=lo, std=hi). */
+ * (seed, tensor_id, i).  kind 0: uniform [lo, hi); kind 1: normal(mean=lo, std=hi);
+ * kind 2: uniform integers in [lo, hi) written as int32 (token ids). */
 int shp_fill_random(shp_ctx* ctx, float* dptr, uint64_t n, uint64_t seed, uint64_t tensor_id,
                     int32_t kind, float lo, float hi);
 
@@ -169,8 +170,10 @@ typedef struct shp_op_desc {
 int shp_model_num_ops(shp_model* model);
 int shp_model_op(shp_model* model, int index, shp_op_desc* desc);
 int shp_model_num_tensors(shp_model* model);
-/* kind: 0 activation, 1 weight/constant, 2 model input */
+/* kind: 0 activation, 1 weight/constant, 2 model input, 3 view into another tensor */
 int shp_model_tensor(shp_model* model, int id, void** dptr, uint64_t* elems, int32_t* kind);
+/* For a view: the tensor it aliases and its element offset (parent -1 otherwise). */
+int shp_model_tensor_parent(shp_model* model, int id, int32_t* parent, uint64_t* offset);
 
 /* ---- TinyLlama-shaped greedy decode with a KV cache (export_llama.py:269-375 math,
  *      run_llama_spirv.py:194-295 loop, without the full S=64 recompute) ----------- */
@@ -189,6 +192,11 @@ int shp_llama_reset(shp_llama* lm);
  * device logits buffer and the greedy argmax (lowest index on ties) to the device
  * token slot; advances the position. Asynchronous. */
 int shp_llama_step(shp_llama* lm, int32_t token);
+/* Runs n_steps tokens, each fed by the previous step's on-device argmax (no host round
+ * trip between tokens).  Asynchronous. */
+int shp_llama_decode(shp_llama* lm, int32_t n_steps);
+/* Synchronises and copies the argmax of every step so far (one per step, in order). */
+int shp_llama_tokens(shp_llama* lm, int32_t* out, int32_t cap, int32_t* n_out);
 /* Feeds prompt[0..n_prompt) then generates n_new greedy tokens into out_tokens
  * (synchronous).  Stops early at token 2 (EOS) or 0 (PAD) like run_llama_spirv.py:292-294;
  * returns the number written through *n_out. */
@@ -196,8 +204,9 @@ int shp_llama_generate(shp_llama* lm, const int32_t* prompt, int32_t n_prompt, i
                        int32_t* out_tokens, int32_t* n_out);
 int shp_llama_use_graph(shp_llama* lm, int enable);
 int shp_llama_logits(shp_llama* lm, void** dptr, uint64_t* elems);
-/* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head",
- * or per layer "attn_norm","wq","wk","wv","wo","ffn_norm","w_gate","w_up","w_down".
+/* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head"
+ * [vocab,hidden], or per layer "attn_norm", "wqkv" (rows q | k | v), "wo", "ffn_norm",
+ * "w_gate_up" (rows interleaved: 2n = gate n, 2n+1 = up n), "w_down".
  * Projection matrices are stored row-major [out,in], the transpose of export_llama.py's
  * [in,out] (`.T` at :203-217,238): one output's weights are contiguous for the GEMV. */
 int shp_llama_weight(shp_llama* lm, int32_t layer, const char* which, void** dptr,

@@ -570,7 +570,7 @@ static const char* kNames[] = {
     "softmax10", "softmax1000", "global_avg_pool_nhwc", "softmax_rows", "layernorm_rows",
     "rmsnorm_rows", "hlo_conv_nhwc_hwio", "conv2d", "fully_connected", "hlo_dot_batched",
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
-    "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows"};
+    "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -811,6 +811,19 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
             out[n] = acc;
         }
         epilogue(out, n_out, 0, bias, residual, act, alpha);
+        return 0;
+    }
+    if (!strcmp(name, "gather_rows")) { /* embed_table[ids] (run_llama_spirv.py:203) */
+        NEED(3);
+        int nid = push[0], len = push[1], rows = push[2];
+        TOTAL((int64_t)nid * len);
+        for (int r = 0; r < nid; ++r) {
+            int32_t id;
+            memcpy(&id, &in0[r], 4);
+            for (int c = 0; c < len; ++c)
+                out[(int64_t)r * len + c] =
+                    (id >= 0 && id < rows) ? in1[(int64_t)id * len + c] : 0.0f;
+        }
         return 0;
     }
     if (!strcmp(name, "argmax_rows")) { /* numpy argmax: first maximum; stored as int32 */

@@ -103,11 +103,16 @@ SIGNATURES = [
     ("shp_model_num_tensors", C.c_int, [C.c_void_p]),
     ("shp_model_tensor", C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_void_p),
                                    C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
+    ("shp_model_tensor_parent", C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int32),
+                                          C.POINTER(C.c_uint64)]),
     ("shp_llama_create", C.c_int, [C.c_void_p, C.POINTER(LlamaConfig), C.c_uint64,
                                    C.POINTER(C.c_void_p)]),
     ("shp_llama_destroy", None, [C.c_void_p]),
     ("shp_llama_reset", C.c_int, [C.c_void_p]),
     ("shp_llama_step", C.c_int, [C.c_void_p, C.c_int32]),
+    ("shp_llama_decode", C.c_int, [C.c_void_p, C.c_int32]),
+    ("shp_llama_tokens", C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32,
+                                   C.POINTER(C.c_int32)]),
     ("shp_llama_generate", C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32,
                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("shp_llama_use_graph", C.c_int, [C.c_void_p, C.c_int]),

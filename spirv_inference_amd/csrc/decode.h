@@ -35,6 +35,9 @@ int attention_decode_launch(hipStream_t s, const float* qkv, float* k_cache, flo
                             int n_heads, int n_kv, int head_dim, int max_seq, float theta,
                             const DecodeState* st, float* out);
 
+// state.token = token (a kernel argument, so no host buffer is involved).
+int set_token_launch(hipStream_t s, DecodeState* st, int32_t token);
+
 // Greedy argmax of logits (lowest index on ties) into state.token and
 // state.out_tokens[state.step]; advances pos and step.
 int argmax_advance_launch(hipStream_t s, const float* logits, int n, DecodeState* st);

@@ -317,6 +317,14 @@ int attention_decode_launch(hipStream_t s, const float* qkv, float* k_cache, flo
     return SHP_OK;
 }
 
+__global__ void set_token_kernel(DecodeState* st, int32_t token) { st->token = token; }
+
+int set_token_launch(hipStream_t s, DecodeState* st, int32_t token) {
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, s, st, token);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
 int argmax_advance_launch(hipStream_t s, const float* logits, int n, DecodeState* st) {
     hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, s, logits, n, st);
     SHP_HIP_CHECK(hipGetLastError());

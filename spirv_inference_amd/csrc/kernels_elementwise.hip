@@ -477,6 +477,35 @@ int launch_bias_act(const shp::Launch& l) {
     return SHP_OK;
 }
 
+// ---- gather_rows (native): out[i][:] = table[ids[i]][:] — the embedding lookup the
+// reference does in numpy (run_llama_spirv.py:203).  push {n_ids, row_len, n_rows};
+// in0 = int32 ids, in1 = table.  An id outside [0, n_rows) yields a zero row (no read).
+__global__ __launch_bounds__(kBlock) void gather_rows_kernel(const int32_t* __restrict__ ids,
+                                                             const float* __restrict__ table,
+                                                             float* __restrict__ y, int n_ids,
+                                                             int row_len, int n_rows) {
+    uint64_t total = (uint64_t)n_ids * row_len;
+    uint64_t stride = (uint64_t)gridDim.x * kBlock;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += stride) {
+        int r = (int)(i / row_len), c = (int)(i % row_len);
+        int id = ids[r];
+        y[i] = (id >= 0 && id < n_rows) ? table[(uint64_t)id * row_len + c] : 0.0f;
+    }
+}
+
+int launch_gather_rows(const shp::Launch& l) {
+    if (l.n_push < 3) return shp::fail(SHP_ERR_PUSH, "gather_rows needs {n_ids, row_len, n_rows}");
+    if (l.push[0] <= 0 || l.push[1] <= 0 || l.push[2] <= 0)
+        return shp::fail(SHP_ERR_SHAPE, "gather_rows: dims");
+    int rc = shp::check_total(l, (int64_t)l.push[0] * l.push[1], "gather_rows");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(ew_grid(l.out_elems)), dim3(kBlock), 0, l.stream,
+                       (const int32_t*)l.in0, (const float*)l.in1, (float*)l.out, l.push[0],
+                       l.push[1], l.push[2]);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
 // ---- counter-based RNG fill ----------------------------------------------------------
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
@@ -494,6 +523,10 @@ __global__ __launch_bounds__(kBlock) void fill_random_kernel(float* __restrict__
         if (kind == 0) {
             float u = (float)(h >> 40) * (1.0f / 16777216.0f);
             p[i] = lo + (hi - lo) * u;
+        } else if (kind == 2) {  // uniform integers in [lo, hi) stored as int32
+            int64_t span = (int64_t)hi - (int64_t)lo;
+            int32_t v = (int32_t)((int64_t)lo + (int64_t)((h >> 11) % (uint64_t)span));
+            reinterpret_cast<int32_t*>(p)[i] = v;
         } else {
             float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f);        // (0, 1]
             float u2 = (float)((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);  // [0, 1)
@@ -510,7 +543,8 @@ namespace shp {
 int fill_random(hipStream_t stream, float* p, uint64_t n, uint64_t seed, uint64_t tensor_id,
                 int kind, float lo, float hi) {
     if (!p && n) return fail(SHP_ERR_INVALID, "fill_random: null pointer");
-    if (kind != 0 && kind != 1) return fail(SHP_ERR_INVALID, "fill_random: kind must be 0 or 1");
+    if (kind < 0 || kind > 2) return fail(SHP_ERR_INVALID, "fill_random: kind must be 0, 1 or 2");
+    if (kind == 2 && !(hi > lo)) return fail(SHP_ERR_INVALID, "fill_random: empty int range");
     if (n == 0) return SHP_OK;
     // Host-side mirror of mix64 for the per-tensor key.
     auto hmix = [](uint64_t z) {
@@ -561,6 +595,7 @@ KernelEntry kElementwiseKernels[] = {
     {"l2_normalization", 1, false, launch_l2_normalization},
     {"broadcast_binary", 14, false, launch_broadcast_binary},
     {"bias_act", 2, true, launch_bias_act},
+    {"gather_rows", 3, false, launch_gather_rows},
 };
 const int kElementwiseKernelCount = sizeof(kElementwiseKernels) / sizeof(kElementwiseKernels[0]);
 

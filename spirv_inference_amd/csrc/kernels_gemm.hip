@@ -1,4 +1,5 @@
 // Dense contractions on the fp32 matrix cores of gfx950 (v_mfma_f32_32x32x2_f32).
+#include "model.h"
 //
 // One implicit-GEMM kernel template serves every dense kernel of the reference:
 //   hlo_conv_nhwc_hwio  kernels/hlo_conv_nhwc_hwio/glsl/hlo_conv_nhwc_hwio.comp:25-49
@@ -526,6 +527,31 @@ size_t gemm_workspace_bytes(const GemmParams& p, int, int, int) {
     SplitPlan sp = plan_split(p, t, nbatch);
     if (sp.splits <= 1) return 0;
     return (size_t)sp.splits * nbatch * p.M * p.N * sizeof(float);
+}
+
+size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
+    GemmParams p;
+    memset(&p, 0, sizeof(p));
+    p.batch_outer = p.batch_inner = 1;
+    std::string k = name ? name : "";
+    if (k == "hlo_conv_nhwc_hwio" && n >= 14) {
+        p.M = q[0] * q[7] * q[8]; p.N = q[6]; p.K = q[4] * q[5] * q[3];
+    } else if ((k == "conv2d" || k == "conv2d_nhwc") && n >= 15) {
+        p.M = q[0] * q[5] * q[6]; p.N = q[4]; p.K = q[1] * q[7] * q[8];
+    } else if (k == "fully_connected" && n >= 4) {
+        if (q[0] <= 8) return 0;
+        p.M = q[0]; p.N = q[2]; p.K = q[1];
+    } else if (k == "hlo_dot_batched" && n >= 5) {
+        p.batch_outer = q[0]; p.M = q[1]; p.K = q[2]; p.N = q[3];
+    } else if (k == "hlo_dot_rank2" && n >= 4) {
+        p.M = q[0]; p.K = q[1]; p.N = q[2];
+    } else if (k == "dot_general_strided" && n >= 17) {
+        p.batch_outer = q[0]; p.batch_inner = q[1]; p.M = q[2]; p.N = q[3]; p.K = q[4];
+    } else {
+        return 0;
+    }
+    if (p.M <= 0 || p.N <= 0 || p.K <= 0) return 0;
+    return gemm_workspace_bytes(p, 0, 0, 0);
 }
 
 int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
