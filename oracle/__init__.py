@@ -82,14 +82,18 @@ def _f32(a) -> np.ndarray:
 def run(name: str, in0, in1, n_out: int, push: Sequence[int], bias=None, residual=None,
         act: str | int = 0, alpha: float = 0.0) -> np.ndarray:
     """Run one reference kernel on the CPU; returns the output as float32."""
-    a0 = _f32(in0) if in0 is not None else np.zeros(1, np.float32)
-    a1 = _f32(in1) if in1 is not None else np.zeros(1, np.float32)
+    # an absent binding is NULL (optional inputs such as softmax_rows' mask test for it)
+    a0 = _f32(in0) if in0 is not None else None
+    a1 = _f32(in1) if in1 is not None else None
     b = _f32(bias) if bias is not None else None
     r = _f32(residual) if residual is not None else None
     out = np.zeros(max(1, n_out), dtype=np.float32)
     parr = (C.c_int32 * max(1, len(push)))(*[int(p) for p in push])
     act_code = ACT[act] if isinstance(act, str) else int(act)
-    rc = lib().orc_run_kernel(name.encode(), a0.ctypes.data, a0.size, a1.ctypes.data, a1.size,
+    rc = lib().orc_run_kernel(name.encode(), a0.ctypes.data if a0 is not None else None,
+                              a0.size if a0 is not None else 0,
+                              a1.ctypes.data if a1 is not None else None,
+                              a1.size if a1 is not None else 0,
                               out.ctypes.data, n_out, parr, len(push),
                               b.ctypes.data if b is not None else None,
                               r.ctypes.data if r is not None else None, act_code, alpha)

@@ -25,7 +25,6 @@ namespace {
 using shp::GemmParams;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BK = 32;      // K tile
 constexpr int KTAB = 1024;  // im2col offset table entries (scalar conv modes)
 
 struct ConvRow {
@@ -71,7 +70,7 @@ __device__ __forceinline__ void conv_k(const GemmParams& p, int k, int amode, in
     }
 }
 
-template <int BM, int BN, int WM, int WN, int AM, int BMD, int CM>
+template <int BM, int BN, int WM, int WN, int BK, int AM, int BMD, int CM>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     constexpr int FM = BM / WM / 32;
     constexpr int FN = BN / WN / 32;
@@ -81,13 +80,27 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     constexpr bool A_CONV = (AM == shp::A_CONV_NHWC4 || AM == shp::A_CONV_NHWC ||
                              AM == shp::A_CONV_NCHW);
     constexpr bool A_TAB = (AM == shp::A_CONV_NHWC || AM == shp::A_CONV_NCHW);
-    constexpr int NA = A_VEC ? BM / 32 : BM / 8;              // A loads per thread
-    constexpr int NB = (BMD == shp::B_STRIDED) ? BN / 8 : BN / 32;  // B loads per thread
-    constexpr int AP = 4, BP = 4;
+    static_assert(BK == 16 || BK == 32, "K tile of 16 or 32");
+    constexpr int KQ = BK / 4;                                        // float4 per A row
+    constexpr int NA = A_VEC ? BM * BK / 1024 : BM * BK / 256;        // A loads per thread
+    constexpr int NB = (BMD == shp::B_STRIDED) ? BN * BK / 256 : BN * BK / 1024;  // B loads
+    constexpr int AP = 4, BP = 4, CP = 4;
+    constexpr int AS = BK + AP;        // A tile row stride (floats)
+    constexpr int BS = BN + BP;        // B tile row stride
+    constexpr int CS = BN + CP;        // C tile row stride (epilogue)
+    constexpr int A_FLOATS = 2 * BM * AS;
+    constexpr int B_FLOATS = 2 * BK * BS;
+    constexpr int SMEM = A_FLOATS + B_FLOATS;
+    // epilogue: the output tile goes through LDS in chunks of RC rows (multiple of 32)
+    constexpr int RC = BM * CS <= SMEM ? BM : (BM / 2) * CS <= SMEM ? BM / 2 : 32;
+    static_assert(RC >= 32 && BM % RC == 0, "epilogue chunk must hold whole 32-row blocks");
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM][BK + AP];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][BN + BP];
+    // One LDS allocation: double-buffered A [2][BM][AS] and B [2][BK][BS] tiles during the
+    // K loop, reused as the [BM][CS] output tile by the epilogue.
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
     __shared__ int2 ktab[A_TAB ? KTAB : 1];
+    float* const As = smem;
+    float* const Bs = smem + A_FLOATS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -113,15 +126,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     const int kbeg = split * p.k_per_split;
     const int kend = min(p.K, kbeg + p.k_per_split);
     const int ntk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    // NHWC with IC a multiple of the K tile: a whole K tile sits inside one (ky, kx) tap,
+    // so its decomposition is uniform across the workgroup (scalar ALU, no per-lane divide).
+    const bool tap_uniform = (AM == shp::A_CONV_NHWC4) && (p.cic % BK == 0) && (kbeg % BK == 0);
 
     // ---- per-thread load coordinates
-    // A: vector modes -> row = tid/8 + 32*j, kq = (tid%8)*4; scalar modes -> m = tid%BM,
-    //    k = tid/BM + (256/BM)*j.
+    // A: vector modes -> row = tid/KQ + (256/KQ)*j, kq = (tid%KQ)*4; scalar modes ->
+    //    m = tid%BM, k = tid/BM + (256/BM)*j.
     ConvRow crow[A_CONV ? (A_VEC ? NA : 1) : 1];
     if constexpr (A_CONV) {
         if constexpr (A_VEC) {
 #pragma unroll
-            for (int j = 0; j < NA; ++j) crow[j] = conv_row(p, m0 + tid / 8 + 32 * j, AM);
+            for (int j = 0; j < NA; ++j) crow[j] = conv_row(p, m0 + tid / KQ + (256 / KQ) * j, AM);
         } else {
             crow[0] = conv_row(p, m0 + tid % BM, AM);
         }
@@ -147,12 +163,12 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     auto load_a = [&](int kt) {
         const int kt0 = kbeg + kt * BK;
         if constexpr (A_VEC) {
-            const int kq = (tid & 7) * 4;
+            const int kq = (tid % KQ) * 4;
             const int k = kt0 + kq;
             if constexpr (AM == shp::A_KVEC) {
 #pragma unroll
                 for (int j = 0; j < NA; ++j) {
-                    int m = m0 + tid / 8 + 32 * j;
+                    int m = m0 + tid / KQ + (256 / KQ) * j;
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (m < p.M && k < kend)
                         v = *reinterpret_cast<const float4*>(A + (int64_t)m * p.sam + k);
@@ -160,13 +176,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
                 }
             } else {  // A_CONV_NHWC4
                 int off = 0, ky = 0, kx = 0;
-                if (k < kend) conv_k(p, k, AM, off, ky, kx);
+                if (tap_uniform) {
+                    int ic0 = kt0 % p.cic;
+                    int t = kt0 / p.cic;
+                    kx = t % p.ckw;
+                    ky = t / p.ckw;
+                    off = (ky * p.ciw + kx) * p.cic + ic0 + kq;
+                } else if (k < kend) {
+                    conv_k(p, k, AM, off, ky, kx);
+                }
 #pragma unroll
                 for (int j = 0; j < NA; ++j) {
                     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                     int iy = crow[j].iy0 + ky, ix = crow[j].ix0 + kx;
-                    if (crow[j].valid && k < kend && iy >= 0 && iy < p.cih && ix >= 0 &&
-                        ix < p.ciw)
+                    if (crow[j].valid && k < kend && (unsigned)iy < (unsigned)p.cih &&
+                        (unsigned)ix < (unsigned)p.ciw)
                         v = *reinterpret_cast<const float4*>(A + crow[j].base + off);
                     ra[j] = v;
                 }
@@ -193,7 +217,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
                             conv_k(p, k, AM, off, ky, kx);
                         }
                         int iy = crow[0].iy0 + ky, ix = crow[0].ix0 + kx;
-                        if (iy >= 0 && iy < p.cih && ix >= 0 && ix < p.ciw)
+                        if ((unsigned)iy < (unsigned)p.cih && (unsigned)ix < (unsigned)p.ciw)
                             v = A[crow[0].base + off];
                     }
                 }
@@ -203,15 +227,16 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     };
 
     auto store_a = [&](int buf) {
+        float* a = As + buf * BM * AS;
         if constexpr (A_VEC) {
-            const int kq = (tid & 7) * 4;
+            const int kq = (tid % KQ) * 4;
 #pragma unroll
             for (int j = 0; j < NA; ++j)
-                *reinterpret_cast<float4*>(&As[buf][tid / 8 + 32 * j][kq]) = ra[j];
+                *reinterpret_cast<float4*>(&a[(tid / KQ + (256 / KQ) * j) * AS + kq]) = ra[j];
         } else {
             const int ml = tid % BM;
 #pragma unroll
-            for (int j = 0; j < NA; ++j) As[buf][ml][tid / BM + (256 / BM) * j] = rs[j];
+            for (int j = 0; j < NA; ++j) a[ml * AS + tid / BM + (256 / BM) * j] = rs[j];
         }
     };
 
@@ -251,26 +276,27 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     };
 
     auto store_b = [&](int buf) {
+        float* b = Bs + buf * BK * BS;
         if constexpr (BMD == shp::B_NVEC) {
             constexpr int TPR = BN / 4;
             const int nl = (tid % TPR) * 4;
 #pragma unroll
             for (int j = 0; j < NB; ++j)
-                *reinterpret_cast<float4*>(&Bs[buf][tid / TPR + (256 / TPR) * j][nl]) = rb[j];
+                *reinterpret_cast<float4*>(&b[(tid / TPR + (256 / TPR) * j) * BS + nl]) = rb[j];
         } else if constexpr (BMD == shp::B_KVEC) {
             const int nl = tid % BN;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 int kl = (tid / BN) * 4 + (256 / BN) * 4 * j;
-                Bs[buf][kl + 0][nl] = rb[j].x;
-                Bs[buf][kl + 1][nl] = rb[j].y;
-                Bs[buf][kl + 2][nl] = rb[j].z;
-                Bs[buf][kl + 3][nl] = rb[j].w;
+                b[(kl + 0) * BS + nl] = rb[j].x;
+                b[(kl + 1) * BS + nl] = rb[j].y;
+                b[(kl + 2) * BS + nl] = rb[j].z;
+                b[(kl + 3) * BS + nl] = rb[j].w;
             }
         } else {
             const int nl = tid % BN;
 #pragma unroll
-            for (int j = 0; j < NB; ++j) Bs[buf][tid / BN + (256 / BN) * j][nl] = rbs[j];
+            for (int j = 0; j < NB; ++j) b[(tid / BN + (256 / BN) * j) * BS + nl] = rbs[j];
         }
     };
 
@@ -297,9 +323,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
                 load_a(kt + 1);
                 load_b(kt + 1);
             }
-            // Lanes 0-31 feed k = s, lanes 32-63 feed k = 16 + s of this K tile: any
+            const float* a = As + buf * BM * AS;
+            const float* b = Bs + buf * BK * BS;
+            // Lanes 0-31 feed k = s, lanes 32-63 feed k = BK/2 + s of this K tile: any
             // assignment works as long as A and B agree, and this one lets each lane read
-            // 16 consecutive k of its A row with 128-bit LDS loads.
+            // BK/2 consecutive k of its A row with 128-bit LDS loads.
 #pragma unroll
             for (int s4 = 0; s4 < BK / 8; ++s4) {
                 float4 af[FM];
@@ -307,22 +335,22 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
                 for (int fm = 0; fm < FM; ++fm)
                     af[fm] = *reinterpret_cast<const float4*>(
-                        &As[buf][arow + fm * 32][lh * 16 + s4 * 4]);
+                        &a[(arow + fm * 32) * AS + lh * (BK / 2) + s4 * 4]);
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        bf[fn][q] = Bs[buf][lh * 16 + s4 * 4 + q][bcol + fn * 32];
+                        bf[fn][q] = b[(lh * (BK / 2) + s4 * 4 + q) * BS + bcol + fn * 32];
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
                     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
                         for (int fn = 0; fn < FN; ++fn) {
-                            float a = q == 0 ? af[fm].x : q == 1 ? af[fm].y
-                                                        : q == 2 ? af[fm].z : af[fm].w;
+                            float av = q == 0 ? af[fm].x : q == 1 ? af[fm].y
+                                                         : q == 2 ? af[fm].z : af[fm].w;
                             acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                a, bf[fn][q], acc[fm][fn], 0, 0, 0);
+                                av, bf[fn][q], acc[fm][fn], 0, 0, 0);
                         }
             }
             if (kt + 1 < ntk) {
@@ -333,40 +361,95 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
         }
     }
 
-    // ---- epilogue.  Accumulator register r of a 32x32 block holds
-    // row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
+    // ---- epilogue.  Accumulator register r of a 32x32 block holds row
+    // 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.  The tile goes through LDS, RC rows
+    // at a time, so global stores (and residual loads) are 16-byte and row-contiguous.
+    float* Cs = smem;
     const int nbatch = gridDim.z;
     const int hw = p.coh * p.cow;
+    float* __restrict__ C = p.c + bo * p.sc_outer + bi * p.sc_inner;
+    const float* __restrict__ R =
+        p.residual ? p.residual + bo * p.sc_outer + bi * p.sc_inner : nullptr;
+    float* __restrict__ P =
+        p.splits > 1 ? p.partial + ((int64_t)split * nbatch + bz) * p.M * p.N : nullptr;
+    const bool vec = P ? (p.N & 3) == 0
+                       : (CM == shp::C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 &&
+                          (p.N & 3) == 0 && (((uintptr_t)C) & 15) == 0 &&
+                          (!p.bias || (((uintptr_t)p.bias) & 15) == 0) &&
+                          (!R || (((uintptr_t)R) & 15) == 0));
+    constexpr int TPR = BN / 4, RPP = 256 / TPR;
+    const int cl4 = (tid % TPR) * 4;
+    const int col4 = n0 + cl4;
+    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (vec && !P && p.bias && col4 < p.N) bv = *reinterpret_cast<const float4*>(p.bias + col4);
 #pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
+    for (int c0 = 0; c0 < BM; c0 += RC) {
+        if (c0 > 0) __syncthreads();  // the previous chunk has been consumed
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int col = n0 + bcol + fn * 32;
-            if (col >= p.N) continue;
-            float bval = (p.splits <= 1 && p.bias) ? p.bias[col] : 0.0f;
+        for (int fm = 0; fm < FM; ++fm) {
+            const int rb = wm * (BM / WM) + fm * 32;
+            if (rb < c0 || rb >= c0 + RC) continue;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * (BM / WM) + fm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (row >= p.M) continue;
-                float v = acc[fm][fn][r];
-                if (p.splits > 1) {
-                    p.partial[(((int64_t)split * nbatch + bz) * p.M + row) * p.N + col] = v;
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    Cs[(rb - c0 + 8 * (r >> 2) + 4 * lh + (r & 3)) * CS + bcol + fn * 32] =
+                        acc[fm][fn][r];
+        }
+        __syncthreads();
+        if (vec) {
+#pragma unroll 4
+            for (int i = 0; i < RC / RPP; ++i) {
+                const int rl = tid / TPR + RPP * i;
+                const int row = m0 + c0 + rl;
+                if (row >= p.M || col4 >= p.N) continue;
+                float4 v = *reinterpret_cast<const float4*>(&Cs[rl * CS + cl4]);
+                if (P) {
+                    *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
+                    continue;
+                }
+                const int64_t ci = (int64_t)row * p.scm + col4;
+                float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (R) rv = *reinterpret_cast<const float4*>(R + ci);
+                v.x = shpd::apply_act(v.x + bv.x + rv.x, p.act, p.alpha);
+                v.y = shpd::apply_act(v.y + bv.y + rv.y, p.act, p.alpha);
+                v.z = shpd::apply_act(v.z + bv.z + rv.z, p.act, p.alpha);
+                v.w = shpd::apply_act(v.w + bv.w + rv.w, p.act, p.alpha);
+                *reinterpret_cast<float4*>(C + ci) = v;
+            }
+        } else {
+            // scalar path: consecutive threads walk the contiguous direction of C
+            for (int e = tid; e < RC * BN; e += 256) {
+                int rl, cl;
+                if constexpr (CM == shp::C_NCHW) {
+                    rl = e % RC;
+                    cl = e / RC;
+                } else {
+                    rl = e / BN;
+                    cl = e % BN;
+                }
+                const int row = m0 + c0 + rl, col = n0 + cl;
+                if (row >= p.M || col >= p.N) continue;
+                float v = Cs[rl * CS + cl];
+                if (P) {
+                    P[(int64_t)row * p.N + col] = v;
                     continue;
                 }
                 int64_t ci;
                 if constexpr (CM == shp::C_NCHW) {
-                    int img = row / hw, pix = row % hw;
+                    const int img = row / hw, pix = row % hw;
                     ci = ((int64_t)img * p.N + col) * hw + pix;
                 } else {
-                    ci = bo * p.sc_outer + bi * p.sc_inner + (int64_t)row * p.scm +
-                         (int64_t)col * p.scn;
+                    ci = (int64_t)row * p.scm + (int64_t)col * p.scn;
                 }
-                v += bval;
-                if (p.residual) v += p.residual[ci];
-                p.c[ci] = shpd::apply_act(v, p.act, p.alpha);
+                if (p.bias) v += p.bias[col];
+                if (R) v += R[ci];
+                C[ci] = shpd::apply_act(v, p.act, p.alpha);
             }
         }
+    }
 }
+
 
 // Split-K second pass: sum the partials in split order, then the epilogue.
 template <int CM>
@@ -446,87 +529,144 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
 
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
-    int bm, bn;
+    int bm, bn, bk;
 };
 
-template <int BM, int BN, int WM, int WN, int AM, int BMD, int CM>
+// Internal tuning overrides (0 = automatic); set through shp_tune() by experiments only.
+int g_force_tile = 0;    // 1: 128x128, 2: 128x64, 3: 64x64
+int g_force_bk = 0;      // 16 or 32
+int g_force_splits = 0;  // split-K count
+
+template <int BM, int BN, int BK, int AM, int BMD, int CM>
 void launch_tile(hipStream_t s, const GemmParams& p, dim3 grid) {
-    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, WM, WN, AM, BMD, CM>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_mfma_kernel<BM, BN, 2, 2, BK, AM, BMD, CM>), grid, dim3(256), 0, s, p);
 }
 
-template <int AM, int BMD, int CM>
+// HOT combos (the model paths) get the BK=16 variants as well.
+template <int AM, int BMD, int CM, bool HOT>
 void launch_combo(hipStream_t s, const GemmParams& p, TileCfg t, dim3 grid) {
-    if (t.bm == 128 && t.bn == 128)
-        launch_tile<128, 128, 2, 2, AM, BMD, CM>(s, p, grid);
-    else if (t.bm == 128 && t.bn == 64)
-        launch_tile<128, 64, 2, 2, AM, BMD, CM>(s, p, grid);
-    else
-        launch_tile<64, 64, 2, 2, AM, BMD, CM>(s, p, grid);
+    if constexpr (HOT) {
+        if (t.bk == 16) {
+            if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128, 16, AM, BMD, CM>(s, p, grid);
+            if (t.bm == 128 && t.bn == 64) return launch_tile<128, 64, 16, AM, BMD, CM>(s, p, grid);
+            return launch_tile<64, 64, 16, AM, BMD, CM>(s, p, grid);
+        }
+    }
+    if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128, 32, AM, BMD, CM>(s, p, grid);
+    if (t.bm == 128 && t.bn == 64) return launch_tile<128, 64, 32, AM, BMD, CM>(s, p, grid);
+    return launch_tile<64, 64, 32, AM, BMD, CM>(s, p, grid);
+}
+
+bool combo_is_hot(int am, int bm, int cm) {
+    using namespace shp;
+    return cm == C_STRIDED && ((am == A_CONV_NHWC4 && bm == B_NVEC) ||
+                               (am == A_CONV_NHWC4 && bm == B_KVEC) ||
+                               (am == A_KVEC && bm == B_NVEC) || (am == A_KVEC && bm == B_KVEC));
 }
 
 int dispatch_combo(hipStream_t s, const GemmParams& p, int am, int bm, int cm, TileCfg t,
                    dim3 grid) {
     using namespace shp;
-#define SHP_COMBO(A_, B_, C_)                       \
-    if (am == A_ && bm == B_ && cm == C_) {          \
-        launch_combo<A_, B_, C_>(s, p, t, grid);    \
-        return SHP_OK;                              \
+#define SHP_COMBO(A_, B_, C_, HOT_)                      \
+    if (am == A_ && bm == B_ && cm == C_) {               \
+        launch_combo<A_, B_, C_, HOT_>(s, p, t, grid);   \
+        return SHP_OK;                                   \
     }
-    SHP_COMBO(A_CONV_NHWC4, B_NVEC, C_STRIDED)
-    SHP_COMBO(A_CONV_NHWC4, B_KVEC, C_STRIDED)
-    SHP_COMBO(A_CONV_NHWC4, B_STRIDED, C_STRIDED)
-    SHP_COMBO(A_CONV_NHWC, B_NVEC, C_STRIDED)
-    SHP_COMBO(A_CONV_NHWC, B_KVEC, C_STRIDED)
-    SHP_COMBO(A_CONV_NHWC, B_STRIDED, C_STRIDED)
-    SHP_COMBO(A_CONV_NCHW, B_KVEC, C_NCHW)
-    SHP_COMBO(A_CONV_NCHW, B_STRIDED, C_NCHW)
-    SHP_COMBO(A_KVEC, B_NVEC, C_STRIDED)
-    SHP_COMBO(A_KVEC, B_KVEC, C_STRIDED)
-    SHP_COMBO(A_KVEC, B_STRIDED, C_STRIDED)
-    SHP_COMBO(A_STRIDED, B_NVEC, C_STRIDED)
-    SHP_COMBO(A_STRIDED, B_KVEC, C_STRIDED)
-    SHP_COMBO(A_STRIDED, B_STRIDED, C_STRIDED)
+    SHP_COMBO(A_CONV_NHWC4, B_NVEC, C_STRIDED, true)
+    SHP_COMBO(A_CONV_NHWC4, B_KVEC, C_STRIDED, true)
+    SHP_COMBO(A_CONV_NHWC4, B_STRIDED, C_STRIDED, false)
+    SHP_COMBO(A_CONV_NHWC, B_NVEC, C_STRIDED, false)
+    SHP_COMBO(A_CONV_NHWC, B_KVEC, C_STRIDED, false)
+    SHP_COMBO(A_CONV_NHWC, B_STRIDED, C_STRIDED, false)
+    SHP_COMBO(A_CONV_NCHW, B_KVEC, C_NCHW, false)
+    SHP_COMBO(A_CONV_NCHW, B_STRIDED, C_NCHW, false)
+    SHP_COMBO(A_KVEC, B_NVEC, C_STRIDED, true)
+    SHP_COMBO(A_KVEC, B_KVEC, C_STRIDED, true)
+    SHP_COMBO(A_KVEC, B_STRIDED, C_STRIDED, false)
+    SHP_COMBO(A_STRIDED, B_NVEC, C_STRIDED, false)
+    SHP_COMBO(A_STRIDED, B_KVEC, C_STRIDED, false)
+    SHP_COMBO(A_STRIDED, B_STRIDED, C_STRIDED, false)
 #undef SHP_COMBO
     return fail(SHP_ERR_UNSUPPORTED, "gemm: unsupported operand mode combination");
 }
 
-TileCfg pick_tile(const GemmParams& p) {
-    int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-    if (p.N <= 64) return {128, 64};
-    if (t128 >= 256 || p.M > 4096) return {128, 128};
-    return {64, 64};
-}
-
-struct SplitPlan {
+struct Plan {
+    TileCfg t;
     int splits, kps;
 };
 
-SplitPlan plan_split(const GemmParams& p, TileCfg t, int nbatch) {
+// Workgroups resident per CU, as the compiler reports them for each variant (LDS of the
+// double-buffered tiles out of 160 KiB per CU, and the VGPR+AGPR budget).
+int occupancy(TileCfg t) {
+    if (t.bm == 128 && t.bn == 128) return t.bk == 16 ? 4 : 2;
+    if (t.bm == 128) return t.bk == 16 ? 4 : 3;
+    return t.bk == 16 ? 8 : 4;
+}
+
+// Relative MFMA efficiency of a tile shape and K tile (fitted to per-layer sweeps of the
+// ResNet-50 convolutions on MI355X).
+double tile_eff(TileCfg t) {
+    double e = (t.bm == 128 && t.bn == 128) ? 1.0 : 0.85;
+    return t.bk == 16 ? e * 0.85 : e;
+}
+
+// Estimated time of a plan: the busiest CU's MFMA work at the utilisation its resident
+// workgroup count allows (more resident waves hide more load latency), plus the split-K
+// reduction pass.
+double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps) {
+    static const double kUtil[8] = {0.4, 0.6, 0.75, 0.85, 0.9, 0.92, 0.95, 1.0};
+    const double cu_rate = 256.0 * 2.4e9;  // fp32 MFMA FLOP/s per CU
     int64_t tiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * nbatch;
-    SplitPlan sp{1, ((p.K + BK - 1) / BK) * BK};
-    if (tiles >= 192 || p.K < 512) return sp;
-    int want = (int)((512 + tiles - 1) / tiles);
-    int maxs = p.K / 256;
-    if (want > maxs) want = maxs;
-    if (want > 16) want = 16;
-    if (want < 2) return sp;
-    int kps = (p.K + want - 1) / want;
-    kps = ((kps + BK - 1) / BK) * BK;
-    sp.kps = kps;
-    sp.splits = (p.K + kps - 1) / kps;
-    return sp;
+    int64_t wgs = tiles * splits;
+    int64_t per_cu = (wgs + 255) / 256;
+    int resident = (int)std::min<int64_t>(occupancy(t), per_cu);
+    double util = kUtil[std::min(resident, 8) - 1];
+    double wg_flops = 2.0 * t.bm * t.bn * kps;
+    double cost = per_cu * wg_flops / (cu_rate * tile_eff(t) * util);
+    if (splits > 1) cost += (splits + 1.0) * p.M * (double)p.N * nbatch * 4.0 / 3.0e12 + 2.0e-6;
+    return cost;
+}
+
+Plan plan_gemm(const GemmParams& p, int nbatch, bool hot) {
+    static const int kTiles[3][2] = {{128, 128}, {128, 64}, {64, 64}};
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    Plan best{{128, 128, 32}, 1, 0};
+    double best_cost = 1e30;
+    for (int ti = 0; ti < 3; ++ti) {
+        if (g_force_tile && g_force_tile != ti + 1) continue;
+        for (int bk : {32, 16}) {
+            if (bk == 16 && !hot) continue;
+            if (g_force_bk && g_force_bk != bk) continue;
+            TileCfg t{kTiles[ti][0], kTiles[ti][1], bk};
+            for (int s : kSplits) {
+                if (g_force_splits && g_force_splits != s) continue;
+                int kps = (p.K + s - 1) / s;
+                kps = ((kps + 31) / 32) * 32;  // a multiple of both K tiles
+                if (kps <= 0) kps = 32;
+                int real = (p.K + kps - 1) / kps;
+                if (s > 1 && (real != s || kps < 128)) continue;
+                double c = plan_cost(p, nbatch, t, s, kps);
+                if (c < best_cost * 0.97) {  // prefer the earlier (simpler) plan on near ties
+                    best_cost = c;
+                    best = Plan{t, s, kps};
+                }
+            }
+        }
+    }
+    if (best.kps <= 0) best.kps = ((p.K + 31) / 32) * 32;
+    if (best.kps <= 0) best.kps = 32;
+    return best;
 }
 
 }  // namespace
 
 namespace shp {
 
-size_t gemm_workspace_bytes(const GemmParams& p, int, int, int) {
-    TileCfg t = pick_tile(p);
+size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode) {
     int nbatch = p.batch_outer * p.batch_inner;
-    SplitPlan sp = plan_split(p, t, nbatch);
-    if (sp.splits <= 1) return 0;
-    return (size_t)sp.splits * nbatch * p.M * p.N * sizeof(float);
+    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode));
+    if (pl.splits <= 1) return 0;
+    return (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
 }
 
 size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
@@ -534,13 +674,19 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
     memset(&p, 0, sizeof(p));
     p.batch_outer = p.batch_inner = 1;
     std::string k = name ? name : "";
+    // the hot combination is the one the model graphs use (NHWC conv / row-major dots)
+    int am = A_KVEC, bm = B_NVEC;
     if (k == "hlo_conv_nhwc_hwio" && n >= 14) {
         p.M = q[0] * q[7] * q[8]; p.N = q[6]; p.K = q[4] * q[5] * q[3];
+        am = A_CONV_NHWC4;
     } else if ((k == "conv2d" || k == "conv2d_nhwc") && n >= 15) {
         p.M = q[0] * q[5] * q[6]; p.N = q[4]; p.K = q[1] * q[7] * q[8];
+        am = A_CONV_NHWC4;
+        bm = B_KVEC;
     } else if (k == "fully_connected" && n >= 4) {
         if (q[0] <= 8) return 0;
         p.M = q[0]; p.N = q[2]; p.K = q[1];
+        bm = B_KVEC;
     } else if (k == "hlo_dot_batched" && n >= 5) {
         p.batch_outer = q[0]; p.M = q[1]; p.K = q[2]; p.N = q[3];
     } else if (k == "hlo_dot_rank2" && n >= 4) {
@@ -551,7 +697,9 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
         return 0;
     }
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) return 0;
-    return gemm_workspace_bytes(p, 0, 0, 0);
+    // the largest of the hot and generic plans, so either launch finds its partials
+    return std::max(gemm_workspace_bytes(p, am, bm, C_STRIDED),
+                    gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED));
 }
 
 int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
@@ -561,14 +709,17 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     int nbatch = p.batch_outer * p.batch_inner;
     if (nbatch <= 0 || nbatch > 65535) return fail(SHP_ERR_SHAPE, "gemm: batch out of range");
     if (amode == A_CONV_NHWC4 && p.cic % 4 != 0) amode = A_CONV_NHWC;
-    TileCfg t = pick_tile(p);
-    SplitPlan sp = plan_split(p, t, nbatch);
-    size_t need = sp.splits > 1 ? (size_t)sp.splits * nbatch * p.M * p.N * sizeof(float) : 0;
-    if (sp.splits > 1 && (workspace == nullptr || workspace_bytes < need))
-        sp = SplitPlan{1, ((p.K + BK - 1) / BK) * BK};
-    p.splits = sp.splits;
-    p.k_per_split = sp.kps > 0 ? sp.kps : BK;
-    p.partial = sp.splits > 1 ? workspace : nullptr;
+    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode));
+    size_t need = pl.splits > 1 ? (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float) : 0;
+    if (pl.splits > 1 && (workspace == nullptr || workspace_bytes < need)) {
+        pl.splits = 1;
+        pl.kps = ((p.K + 31) / 32) * 32;
+        if (pl.kps <= 0) pl.kps = 32;
+    }
+    p.splits = pl.splits;
+    p.k_per_split = pl.kps;
+    p.partial = pl.splits > 1 ? workspace : nullptr;
+    TileCfg t = pl.t;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
     if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
     dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
@@ -590,6 +741,16 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
 }
 
 }  // namespace shp
+
+// Internal tuning hook for experiments (not part of include/spirv_hip.h).
+extern "C" int shp_tune(const char* key, int value) {
+    std::string k = key ? key : "";
+    if (k == "gemm_tile") g_force_tile = value;
+    else if (k == "gemm_bk") g_force_bk = value;
+    else if (k == "gemm_splits") g_force_splits = value;
+    else return SHP_ERR_INVALID;
+    return SHP_OK;
+}
 
 namespace {
 

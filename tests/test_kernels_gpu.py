@@ -25,8 +25,9 @@ def f32bits(v):
 
 def hip(ctx, name, in0, in1, n_out, push, bias=None, residual=None, act=0, alpha=0.0,
         out_dtype=np.float32):
-    t0 = ctx.tensor(in0) if in0 is not None else ctx.tensor(np.zeros(1, np.float32))
-    t1 = ctx.tensor(in1) if in1 is not None else ctx.tensor(np.zeros(1, np.float32))
+    # an absent binding is a null pointer, as in the model graphs
+    t0 = ctx.tensor(in0) if in0 is not None else None
+    t1 = ctx.tensor(in1) if in1 is not None else None
     tb = ctx.tensor(bias) if bias is not None else None
     tr = ctx.tensor(residual) if residual is not None else None
     out = ctx.empty(n_out, out_dtype)

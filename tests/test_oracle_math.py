@@ -164,6 +164,14 @@ def test_softmax_and_norms_vs_float64(orc):
     assert_close(y, ref, 1e-5, 1e-5, "rmsnorm")
 
 
+def test_softmax_rows_without_mask(orc):
+    """An absent mask binding (NULL) means no mask — regression for the optional in1."""
+    x = rnd(2, 1000, scale=5.0)
+    y = orc.run("softmax_rows", x, None, x.size, [2, 1000, 1065353216])  # scale 1.0
+    ref = torch.softmax(torch.from_numpy(x.astype(np.float64)), -1).numpy()
+    assert_close(y, ref, 1e-6, 1e-5, "softmax_rows no mask")
+
+
 def test_gelu_erfc_expansion_vs_exact(orc):
     from scipy.special import erfc
     x = np.linspace(-12, 12, 4001).astype(np.float32)
