@@ -6,10 +6,10 @@ graph, with TinyLlama-1.1B fp32 greedy decode tok/s an
 roofline fractions reported beside it.  Synthetic seeded inputs and random-init weights,
 generated on the device; inputs are resident in HBM before the timed region starts.
 
-Timed region: K forward passes, each op launched on the context stream with a hipEvent
-pair around it (the per-kernel durations give the roofline of the dominant kernel, the
-MFMA implicit-GEMM convolution); host wall clock around the K passes gives value and
-ms_per_step.  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
+Timed region: K forward passes replayed from one hipGraph capture of the step; host wall
+clock around them gives value and ms_per_step.  Profiled region: the same K passes launched
+eagerly with a hipEvent pair around every kernel on the context stream; those per-kernel
+durations give the roofline of the dominant kernel (the MFMA implicit-GEMM convolution).  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
 a bounded sample of the same workload on this box's host cores.
 
 Prints ONE JSON line.  --gpus N > 1 exits with an explanation (single-GPU build).
@@ -43,45 +43,72 @@ def conv_flops(op) -> float:
     return 0.0
 
 
+def conv_bytes(op) -> float:
+    """Algorithmic HBM bytes of one hlo_conv_nhwc_hwio launch: input (only the sampled pixels
+    for a strided 1x1), HWIO weights, output, and the residual read when the epilogue adds one."""
+    q = op.push
+    if op.kernel != "hlo_conv_nhwc_hwio":
+        return 0.0
+    n, ih, iw, ic, kh, kw, oc, oh, ow, sh, sw = q[:11]
+    inp = n * oh * ow * ic if (kh == 1 and kw == 1 and (sh > 1 or sw > 1)) else n * ih * iw * ic
+    out = n * oh * ow * oc
+    return 4.0 * (inp + kh * kw * ic * oc + out * (2 if op.residual >= 0 else 1))
+
+
+def measured_conv_traffic(batch: int):
+    """HBM bytes per conv launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of
+    this workload (profiles/resnet50_b32_conv_layers.md), or None for other batch sizes."""
+    path = os.path.join(ROOT, "profiles", "resnet50_b32_conv_layers.md")
+    if batch != 32 or not os.path.exists(path):
+        return None
+    for ln in open(path):
+        if ln.startswith("hbm_bytes_per_conv_launch"):
+            return float(ln.split("=")[1])
+    return None
+
+
 def bench_resnet(ctx, steps: int, warmup: int, batch: int):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
     flops, wbytes = m.work()
     ops = m.ops()
     cflops = sum(conv_flops(o) for o in ops)
+    cbytes = sum(conv_bytes(o) for o in ops)
     n_conv = sum(1 for o in ops if o.kernel == "hlo_conv_nhwc_hwio")
+    # timed region: the step captured once into a hipGraph and replayed K times
+    m.use_graph(True)
     for _ in range(warmup):
         m.run()
-    ctx.sync()
-    ctx.timing(True)
-    ctx.timing_reset()
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
         m.run()
     ctx.sync()
     t1 = time.perf_counter()
-    rep = ctx.timing_report()
-    ctx.timing(False)
     elapsed = t1 - t0
-    conv_ms, conv_n = rep.get("hlo_conv_nhwc_hwio", (0.0, 0))
-    kernel_ms = sum(v[0] for v in rep.values()) / steps
-    # graph replay of the same step (launch overhead removed), reported beside it
-    m.use_graph(True)
+    # profiled region: the same K steps launched eagerly with a hipEvent pair around every
+    # kernel on the context stream -> per-kernel durations for the roofline
+    m.use_graph(False)
     m.run()
     ctx.sync()
-    g0 = time.perf_counter()
+    ctx.timing(True)
+    ctx.timing_reset()
+    e0 = time.perf_counter()
     for _ in range(steps):
         m.run()
     ctx.sync()
-    g1 = time.perf_counter()
+    e1 = time.perf_counter()
+    rep = ctx.timing_report()
+    ctx.timing(False)
+    conv_ms, conv_n = rep.get("hlo_conv_nhwc_hwio", (0.0, 0))
+    kernel_ms = sum(v[0] for v in rep.values()) / steps
     logits = m.output(1).download().reshape(batch, -1)
     top1 = [int(i) for i in np.argmax(logits, axis=1)]
     achieved = cflops * steps / (conv_ms / 1e3) / 1e12 if conv_ms > 0 else 0.0
     res = dict(
         img_s=batch * steps / elapsed, ms_per_step=elapsed / steps * 1e3,
-        graph_ms_per_step=(g1 - g0) / steps * 1e3, kernel_ms_per_step=kernel_ms,
-        flops_per_img=flops / batch, conv_flops_per_step=cflops, n_conv=n_conv,
+        eager_ms_per_step=(e1 - e0) / steps * 1e3, kernel_ms_per_step=kernel_ms,
+        flops_per_img=flops / batch, conv_flops_per_step=cflops, conv_bytes_per_step=cbytes, n_conv=n_conv,
         conv_ms_per_step=conv_ms / steps, conv_launches=conv_n,
         conv_avg_launch_ms=conv_ms / max(conv_n, 1), achieved_tflops=achieved,
         per_kernel_ms={k: v[0] / steps for k, v in sorted(rep.items())}, top1=top1,
@@ -112,7 +139,10 @@ def bench_decode(ctx, n_new: int, n_prompt: int):
     # KV bytes read per token: K and V of every layer for positions 0..pos
     kv_tok = [2 * cfg["n_layers"] * cfg["n_kv_heads"] * 64 * 4 * (p + 1)
               for p in range(n_prompt, n_prompt + n_new)]
-    bytes_tok = wbytes + float(np.mean(kv_tok))
+    # every weight is streamed once per token except the embedding table, of which one row
+    # is read
+    embed_bytes = cfg["vocab"] * cfg["hidden"] * 4.0
+    bytes_tok = wbytes - embed_bytes + cfg["hidden"] * 4.0 + float(np.mean(kv_tok))
     return dict(tok_s=n_new / (t1 - t0), ms_per_token=s_per_tok * 1e3, bytes_per_token=bytes_tok,
                 achieved_gbs=bytes_tok / s_per_tok / 1e9, prompt=prompt, tokens=gen, lm=lm)
 
@@ -169,10 +199,13 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--prompt-tokens", type=int, default=32)
-    ap.add_argument("--cpu-sample", type=int, default=2, help="images for the CPU baseline")
-    ap.add_argument("--cpu-decode-steps", type=int, default=4)
+    ap.add_argument("--cpu-sample", type=int, default=32, help="images for the CPU baseline")
+    ap.add_argument("--cpu-decode-steps", type=int, default=19,
+                    help="decode steps for the CPU baseline (after the prompt)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="also run one `reshape` copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no collectives or sharding); "
@@ -184,7 +217,7 @@ def main() -> int:
     log(f"device {ctx.device_name}")
     rn = bench_resnet(ctx, args.steps, args.warmup, args.batch)
     log(f"resnet50 b{args.batch}: {rn['img_s']:.1f} img/s, {rn['ms_per_step']:.3f} ms/step "
-        f"(graph {rn['graph_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
+        f"(eager+events {rn['eager_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx, args.decode_tokens, args.prompt_tokens)
@@ -203,7 +236,7 @@ def main() -> int:
             log(f"cpu oracle decode: {cpu_dec['value']:.3f} tok/s "
                 f"(tokens match {cpu_dec['tokens_match']})")
 
-    conv_ms = rn["conv_ms_per_step"]
+    traffic = measured_conv_traffic(args.batch)
     line = {
         "metric": METRIC,
         "value": round(rn["img_s"], 3),
@@ -233,7 +266,10 @@ def main() -> int:
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(rn["achieved_tflops"] / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_unit": "HBM bytes per conv launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, "
+                            "scaled by a 256 MiB copy; profiles/resnet50_b32_conv_layers.md)",
+            "algorithmic_bytes_per_launch": round(rn["conv_bytes_per_step"] / rn["n_conv"]),
             "algorithmic_flops_per_step": rn["conv_flops_per_step"],
             "launches_per_step": rn["n_conv"],
             "avg_launch_ms": round(rn["conv_avg_launch_ms"], 5),
@@ -245,8 +281,9 @@ def main() -> int:
                       f"top-1 identical to the GPU's: {cpu['top1_match']}",
         },
         "extra": {
-            "graph_replay_ms_per_step": round(rn["graph_ms_per_step"], 4),
-            "graph_replay_img_s": round(args.batch / rn["graph_ms_per_step"] * 1e3, 3),
+            "timed_region": "hipGraph replay of the whole step, K times, host clock",
+            "profiled_region": "the same K steps launched eagerly with a hipEvent pair per kernel",
+            "eager_ms_per_step": round(rn["eager_ms_per_step"], 4),
             "kernel_ms_per_step": round(rn["kernel_ms_per_step"], 4),
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},
             "top1": rn["top1"],
@@ -273,6 +310,15 @@ def main() -> int:
                           f"GPU's: {cpu_dec['tokens_match']}"},
         }
         dec["lm"].close()
+    if args.copy_calibration_mb > 0:
+        # a plain copy of known size, so FETCH_SIZE / WRITE_SIZE counters can be scaled
+        n = args.copy_calibration_mb * (1 << 20) // 4
+        src, dst = ctx.empty(n), ctx.empty(n)
+        ctx.fill_random(src, 9, 0, "uniform", 0.0, 1.0)
+        ctx.launch("reshape", src, None, dst, [n])
+        ctx.sync()
+        src.free()
+        dst.free()
     print(json.dumps(line), flush=True)
     ctx.close()
     return 0
