@@ -117,13 +117,7 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int):
     return res
 
 
-def bench_decode(ctx, n_new: int, n_prompt: int):
-    from spirv_inference_amd.models import TINYLLAMA, Llama
-    rng = np.random.default_rng(3)
-    prompt = [int(t) for t in rng.integers(0, TINYLLAMA["vocab"], n_prompt)]
-    lm = Llama(ctx, seed=2)
-    lm.use_graph(True)
-    wbytes = lm.weight_bytes()
+def time_decode(ctx, lm, prompt, n_new: int):
     lm.reset()
     for t in prompt:
         lm.step(t)
@@ -133,8 +127,23 @@ def bench_decode(ctx, n_new: int, n_prompt: int):
     ctx.sync()
     t1 = time.perf_counter()
     toks = lm.tokens()
-    gen = toks[n_prompt - 1:n_prompt - 1 + n_new]
-    s_per_tok = (t1 - t0) / n_new
+    return (t1 - t0) / n_new, toks[len(prompt) - 1:len(prompt) - 1 + n_new]
+
+
+def bench_decode(ctx, n_new: int, n_prompt: int):
+    from spirv_inference_amd.models import TINYLLAMA, Llama
+    rng = np.random.default_rng(3)
+    prompt = [int(t) for t in rng.integers(0, TINYLLAMA["vocab"], n_prompt)]
+    lm = Llama(ctx, seed=2)
+    engine = lm.engine  # the default: persistent where the device allows it
+    wbytes = lm.weight_bytes()
+    # the per-op engine (one hipGraph per token) for comparison, then the default engine
+    lm.set_engine("graph")
+    time_decode(ctx, lm, prompt, 2)
+    graph_s, graph_gen = time_decode(ctx, lm, prompt, n_new)
+    lm.set_engine(engine)
+    time_decode(ctx, lm, prompt, 2)
+    s_per_tok, gen = time_decode(ctx, lm, prompt, n_new)
     cfg = TINYLLAMA
     # KV bytes read per token: K and V of every layer for positions 0..pos
     kv_tok = [2 * cfg["n_layers"] * cfg["n_kv_heads"] * 64 * 4 * (p + 1)
@@ -143,8 +152,9 @@ def bench_decode(ctx, n_new: int, n_prompt: int):
     # is read
     embed_bytes = cfg["vocab"] * cfg["hidden"] * 4.0
     bytes_tok = wbytes - embed_bytes + cfg["hidden"] * 4.0 + float(np.mean(kv_tok))
-    return dict(tok_s=n_new / (t1 - t0), ms_per_token=s_per_tok * 1e3, bytes_per_token=bytes_tok,
-                achieved_gbs=bytes_tok / s_per_tok / 1e9, prompt=prompt, tokens=gen, lm=lm)
+    return dict(tok_s=1.0 / s_per_tok, ms_per_token=s_per_tok * 1e3, bytes_per_token=bytes_tok,
+                achieved_gbs=bytes_tok / s_per_tok / 1e9, prompt=prompt, tokens=gen, lm=lm,
+                engine=engine, graph_tok_s=1.0 / graph_s, graph_tokens_match=graph_gen == gen)
 
 
 def cpu_baseline_resnet(ctx, sample: int, gpu_top1):
@@ -221,7 +231,9 @@ def main() -> int:
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx, args.decode_tokens, args.prompt_tokens)
-        log(f"tinyllama decode: {dec['tok_s']:.1f} tok/s, {dec['achieved_gbs']:.0f} GB/s")
+        log(f"tinyllama decode ({dec['engine']}): {dec['tok_s']:.1f} tok/s, "
+            f"{dec['achieved_gbs']:.0f} GB/s; graph engine {dec['graph_tok_s']:.1f} tok/s "
+            f"(tokens identical {dec['graph_tokens_match']})")
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     cpu = None
     cpu_dec = None
@@ -294,7 +306,7 @@ def main() -> int:
             "workload": "TinyLlama-1.1B-shape fp32 greedy decode, batch 1, 22 layers, hidden 2048, "
                         "32q/4kv heads, SwiGLU 5632, vocab 32000, N(0,0.02) weights, "
                         f"{args.prompt_tokens} seeded prompt ids, {args.decode_tokens} new tokens "
-                        "(KV cache, hipGraph per token)",
+                        "(KV cache; timed: one decode call of the default engine)",
             "value": round(dec["tok_s"], 3), "unit": "tok/s",
             "ms_per_token": round(dec["ms_per_token"], 4),
             "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
@@ -302,6 +314,9 @@ def main() -> int:
                          "frac": round(dec["achieved_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
                          "bytes_per_token": dec["bytes_per_token"]},
             "tokens": dec["tokens"],
+            "engine": dec["engine"],
+            "graph_engine_tok_s": round(dec["graph_tok_s"], 3),
+            "graph_engine_tokens_identical": dec["graph_tokens_match"],
             "cpu_baseline": None if cpu_dec is None else {
                 "value": round(cpu_dec["value"], 4), "unit": "tok/s", "cores": cores,
                 "kind": "port",

@@ -203,6 +203,18 @@ int shp_llama_tokens(shp_llama* lm, int32_t* out, int32_t cap, int32_t* n_out);
 int shp_llama_generate(shp_llama* lm, const int32_t* prompt, int32_t n_prompt, int32_t n_new,
                        int32_t* out_tokens, int32_t* n_out);
 int shp_llama_use_graph(shp_llama* lm, int enable);
+/* Decode engines.  All three compute the same math on the same device state, so they can be
+ * switched between calls.
+ *   SHP_LLAMA_KERNELS     one launch per op (5 per layer + lm_head + argmax), eager;
+ *   SHP_LLAMA_GRAPH       the same launches replayed from a hipGraph per token;
+ *   SHP_LLAMA_PERSISTENT  one cooperative launch per step/decode call: a workgroup per CU
+ *                         streams its share of every layer, phases separated by grid
+ *                         barriers (default where the device and shape allow it).
+ * use_graph(1/0) selects GRAPH/KERNELS.  Selecting PERSISTENT where it is unavailable
+ * returns SHP_ERR_UNSUPPORTED with the reason. */
+enum { SHP_LLAMA_KERNELS = 0, SHP_LLAMA_GRAPH = 1, SHP_LLAMA_PERSISTENT = 2 };
+int shp_llama_set_engine(shp_llama* lm, int engine);
+int shp_llama_engine(shp_llama* lm, int* engine);
 int shp_llama_logits(shp_llama* lm, void** dptr, uint64_t* elems);
 /* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head"
  * [vocab,hidden], or per layer "attn_norm", "wqkv" (rows q | k | v), "wo", "ffn_norm",

@@ -116,6 +116,8 @@ SIGNATURES = [
     ("shp_llama_generate", C.c_int, [C.c_void_p, C.POINTER(C.c_int32), C.c_int32, C.c_int32,
                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("shp_llama_use_graph", C.c_int, [C.c_void_p, C.c_int]),
+    ("shp_llama_set_engine", C.c_int, [C.c_void_p, C.c_int]),
+    ("shp_llama_engine", C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     ("shp_llama_logits", C.c_int, [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
     ("shp_llama_weight", C.c_int, [C.c_void_p, C.c_int32, C.c_char_p, C.POINTER(C.c_void_p),
                                    C.POINTER(C.c_uint64)]),

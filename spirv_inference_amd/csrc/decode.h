@@ -42,4 +42,59 @@ int set_token_launch(hipStream_t s, DecodeState* st, int32_t token);
 // state.out_tokens[state.step]; advances pos and step.
 int argmax_advance_launch(hipStream_t s, const float* logits, int n, DecodeState* st);
 
+// ---- persistent decode: every token of a decode call in one cooperative launch ----------
+struct PersistLayer {
+    const float *attn_norm, *wqkv, *wo, *ffn_norm, *w_gu, *w_down;
+};
+
+struct ArgmaxCand {
+    float value;
+    int32_t index;
+};
+
+struct PersistArgs {
+    const PersistLayer* layers;  // device array [n_layers]
+    const float* embed;
+    const float* final_norm;
+    const float* lm_head;
+    float* k_cache;
+    float* v_cache;
+    float* x;       // [hidden] residual stream
+    float* qkv;     // [(n_heads + 2 n_kv) * 64]
+    float* att;     // [n_heads * 64] attention output
+    float* act;     // [ffn] silu(gate) * up
+    float* logits;  // [vocab]
+    ArgmaxCand* cand;  // [grid] per-workgroup argmax of its logits rows
+    const float* zero_row;  // >= max(hidden, n_heads * 64, ffn) zeros (padding-row loads)
+    DecodeState* st;
+    unsigned long long* bar;  // barrier counters: [0] top, [8 * (1 + g)] group g (monotonic)
+    int* abort_flag;          // set when a barrier wait exceeds spin_limit
+    unsigned long long bar_base;  // top counter value when this launch starts
+    int bar_groups;               // arrival groups; the top counter gains this per barrier
+    long long spin_limit;         // polls of the counter before a wait gives up
+    int n_layers, hidden, n_heads, n_kv, ffn, vocab, max_seq;
+    float eps, theta;
+    int n_tokens;      // tokens decoded by this launch
+    int forced_token;  // >= 0: the first token fed (a prompt id); < 0: state.token
+    // Optional phase timestamps (100 MHz wall clock), null when not profiling:
+    // prof[((token * barriers_per_token + k) * 4 + slot) * grid + workgroup], slot 0 arrival
+    // at barrier k, 1 its pass; in the attention phase 2 = first tile staged.
+    unsigned long long* prof;
+};
+
+// Grid barriers one token costs: five per layer and one before the global argmax.
+inline int persist_barriers_per_token(int n_layers) { return 5 * n_layers + 1; }
+// Arrival groups of the two-level barrier for a grid of `grid` workgroups.
+inline int persist_bar_groups(int grid) { return grid % 16 == 0 ? 16 : 1; }
+// unsigned long long slots the barrier counters occupy.
+constexpr int kPersistBarSlots = 8 * 17;
+
+// Checks that the persistent kernel supports this shape and that the device can keep one
+// workgroup per CU resident.  On success *grid > 0 and *lds is the dynamic LDS size;
+// otherwise *grid = 0 and *why gives the reason.
+int persist_plan(int device, PersistArgs* a, int* grid, size_t* lds, std::string* why);
+
+// One cooperative launch decoding a.n_tokens tokens.
+int persist_launch(hipStream_t s, const PersistArgs& a, int grid, size_t lds);
+
 }  // namespace shp

@@ -1,0 +1,725 @@
+// Persistent batch-1 decode: every token of a decode call in ONE cooperative launch.
+//
+// Same math as the per-op decode kernels (export_llama.py:284-375 with a KV cache): RMSNorm,
+// fused QKV, RoPE, GQA attention, Wo + residual, RMSNorm, SwiGLU gate/up, down + residual,
+// final RMSNorm, lm_head and a greedy argmax that feeds the next token.
+//
+// Why one launch: at batch 1 a token is ~115 small HBM-bound GEMVs.  As separate kernels each
+// pays a launch gap, a ramp and a drain, and those dominate the 2-90 MB reads.  Here one
+// workgroup of 512 threads runs on every CU for the whole call; the phases of a layer are
+// separated by grid barriers (an arrival counter in device memory), and before waiting at a
+// barrier every workgroup already issues the weight loads of its share of the NEXT phase
+// (weights do not depend on the barrier), so HBM keeps streaming while the grid synchronises.
+//
+// Phases of one layer (rows of each matrix split evenly over the workgroups):
+//   A  qkv = Wqkv . rmsnorm(x) * attn_norm
+//   B1 attention, one workgroup per query head (RoPE, online softmax over the cached
+//      positions staged in LDS in 64-position tiles); the workgroup of a group's first query
+//      head appends its K/V to the cache
+//   B2 x[r] += Wo[r] . att
+//   C  act = silu(Wg . h) * (Wu . h), h = rmsnorm(x) * ffn_norm (gate/up rows interleaved)
+//   D  x[r] += Wdown[r] . act
+// After the last layer: E logits = lm_head . rmsnorm(x) * final_norm with a per-workgroup
+// argmax, then F the global argmax (every workgroup reduces the candidates itself).
+// Layer 0 reads the embedding row directly, so no barrier is needed between tokens.
+//
+// Weight rows are streamed with 16-byte non-temporal loads, three chunks deep per thread.
+//
+// Cross-workgroup data (qkv, x, act, the KV cache rows, the argmax candidates) is written and
+// read with agent-scope relaxed atomics, i.e. stores and loads that go to the device-coherent
+// level instead of the per-XCD L2.  A barrier is then only: every wave waits for its stores
+// to complete, one arrival per workgroup on a group counter (16 groups), the last arrival of
+// a group bumps the top counter, and thread 0 polls the top counter.  No L2 write-back or
+// invalidate is needed, which is what makes a barrier ~3 us instead of ~10-30 us on MI355X.
+// Every wait is bounded (spin_limit polls); on expiry the workgroup raises abort_flag and
+// every workgroup exits, so the grid always drains.
+#include <cfloat>
+
+#include "decode.h"
+
+namespace {
+
+using shp::ArgmaxCand;
+using shp::PersistArgs;
+using shp::PersistLayer;
+
+constexpr int NT = 512;  // threads per workgroup
+constexpr int NW = NT / 64;
+constexpr int NB = 8;    // float4 weight slots per thread per chunk
+
+typedef float nfloat4 __attribute__((ext_vector_type(4)));
+// Pointers that arrive through structs are generic; accessing them as global (address space
+// 1) keeps the loads off the flat path, whose completion is also counted by the LDS counter
+// (a flat load in flight would then stall every LDS wait of the reduction).
+#define SHP_GLOBAL __attribute__((address_space(1)))
+
+__device__ __forceinline__ float4 ldw(const float* p) {
+    nfloat4 v = __builtin_nontemporal_load((const SHP_GLOBAL nfloat4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ldw_at(const float* base, unsigned byte_off) {
+    const SHP_GLOBAL char* p = (const SHP_GLOBAL char*)base + byte_off;
+    nfloat4 v = __builtin_nontemporal_load((const SHP_GLOBAL nfloat4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+// Global memory only: the cast to address space 1 would misread an LDS pointer.
+__device__ __forceinline__ float4 ldg4(const float* p) {
+    nfloat4 v = *(const SHP_GLOBAL nfloat4*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+// Device-coherent (agent scope) accesses for data exchanged between workgroups (global
+// memory only, like ldg4).
+__device__ __forceinline__ float ld_coh(const float* p) {
+    return __hip_atomic_load((SHP_GLOBAL float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+    __hip_atomic_store((SHP_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld_coh4(const float* p) {
+    SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)p;
+    unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
+                       __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
+}
+// The same with a uniform base and a 32-bit per-lane byte offset (SGPR-base addressing).
+__device__ __forceinline__ float ld_coh_at(const float* base, unsigned byte_off) {
+    return __hip_atomic_load((SHP_GLOBAL float*)((const SHP_GLOBAL char*)base + byte_off),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld_coh4_at(const float* base, unsigned byte_off) {
+    SHP_GLOBAL unsigned long long* q =
+        (SHP_GLOBAL unsigned long long*)((const SHP_GLOBAL char*)base + byte_off);
+    unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
+                       __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
+}
+__device__ __forceinline__ float dot4(float4 a, float4 b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ void part(int n, int b, int g, int& r0, int& r1) {
+    r0 = (int)((int64_t)n * b / g);
+    r1 = (int)((int64_t)n * (b + 1) / g);
+}
+
+// Sum over the workgroup; `scratch` holds NW floats.  Ends with a barrier so the scratch
+// can be reused immediately.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += scratch[w];
+    __syncthreads();
+    return s;
+}
+
+// Chunk of CH rows [rc, rc + CH) of a row-major [rows][K4] float4 matrix: thread t holds
+// columns t + NT*j (j < J) of each row.  Every slot is loaded unconditionally (a branch would
+// make the register allocator copy the previous chunk's values, which waits for their loads):
+// rows >= r1 read the zero row instead, columns >= K4 are clamped to the last column (the
+// vector slice is zero there).  Row bases are uniform, per-thread offsets 32-bit.
+template <int J, int CH>
+__device__ __forceinline__ void load_chunk(float4 (&b)[NB], const float* __restrict__ W, int K4,
+                                           int rc, int r1, const float* zero_row) {
+    static_assert(J * CH <= NB, "chunk exceeds the slot budget");
+    const unsigned t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const float* row = rc + i < r1 ? W + (size_t)(rc + i) * (size_t)K4 * 4 : zero_row;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const unsigned c = min(t + (unsigned)(NT * j), (unsigned)K4 - 1u);
+            b[i * J + j] = ldw_at(row, c * 16u);
+        }
+    }
+}
+
+// Eight per-thread partial sums -> eight wavefront totals in 10 shuffles: each step halves
+// the values a lane carries while doubling the lanes summed.  Afterwards lane 8r holds the
+// total of row r.
+__device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float keep = b5 ? v[i + 4] : v[i];
+        float send = b5 ? v[i] : v[i + 4];
+        a[i] = keep + __shfl_xor(send, 32);
+    }
+    float c[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float keep = b4 ? a[i + 2] : a[i];
+        float send = b4 ? a[i] : a[i + 2];
+        c[i] = keep + __shfl_xor(send, 16);
+    }
+    float keep = b3 ? c[1] : c[0];
+    float send = b3 ? c[0] : c[1];
+    float w = keep + __shfl_xor(send, 8);
+    w += __shfl_xor(w, 4);
+    w += __shfl_xor(w, 2);
+    w += __shfl_xor(w, 1);
+    return w;
+}
+
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
+
+struct Epi {
+    float* out;
+    const float* resid;  // EPI_RESID: LDS copy of the vector added per row
+    float best;          // EPI_LOGITS: running max / index (thread 0)
+    int best_idx;
+};
+
+// One chunk: partial dot products of the CH rows in `b`, the workgroup reduction, and the
+// epilogue for rows rc..rc+CH-1.  `red` is [2][NW][8] floats, alternated by `rsel`.
+template <int J, int CH, int EPI>
+__device__ __forceinline__ void chunk_step(const float4 (&b)[NB], const float4 (&xv)[J], int rc,
+                                           int r1, float* red, int& rsel, Epi& e) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j) v[i] += dot4(b[i * J + j], xv[j]);
+    float w = reduce8(v, lane);
+    float* rb = red + rsel * (NW * 8);
+    rsel ^= 1;
+    if ((lane & 7) == 0) rb[wave * 8 + (lane >> 3)] = w;
+    __syncthreads();
+    if constexpr (EPI == EPI_SWIGLU) {
+        if (t < CH / 2) {
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) {
+                g += rb[q * 8 + 2 * t];
+                u += rb[q * 8 + 2 * t + 1];
+            }
+            const int r = rc + 2 * t;
+            if (r + 1 < r1) st_coh(e.out + (r >> 1), (g * (1.0f / (1.0f + expf(-g)))) * u);
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        if (t < 64) {  // wave 0: lanes < CH own one row each
+            float s = -FLT_MAX;
+            int idx = 0x7fffffff;
+            const int r = rc + t;
+            if (t < CH && r < r1) {
+                s = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NW; ++q) s += rb[q * 8 + t];
+                e.out[r] = s;
+                idx = r;
+            }
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) {  // rows of the chunk sit in lanes 0..7
+                float os = __shfl_xor(s, o);
+                int oi = __shfl_xor(idx, o);
+                if (os > s || (os == s && oi < idx)) { s = os; idx = oi; }
+            }
+            if (t == 0 && (s > e.best || (s == e.best && idx < e.best_idx))) {
+                e.best = s;
+                e.best_idx = idx;
+            }
+        }
+    } else {
+        if (t < CH) {
+            const int r = rc + t;
+            if (r < r1) {
+                float s = 0.0f;
+#pragma unroll
+                for (int q = 0; q < NW; ++q) s += rb[q * 8 + t];
+                if constexpr (EPI == EPI_RESID) s += e.resid[r];
+                st_coh(e.out + r, s);
+            }
+        }
+    }
+}
+
+// Rows [r0, r1) of W (row-major, K4 float4 per row) against the per-thread vector slice xv.
+// On entry b0 holds chunk 0 and, when PRE == 2, b1 holds chunk 1 (issued by the caller,
+// usually before a barrier); chunk c+2 is issued before chunk c is consumed, in three
+// rotating register sets.
+template <int J, int CH, int EPI, int PRE = 2>
+__device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4, int r0, int r1,
+                                            const float4 (&xv)[J], float4 (&b0)[NB],
+                                            float4 (&b1)[NB], float4 (&b2)[NB], float* red,
+                                            int& rsel, Epi& e, const float* zero_row) {
+    const int nch = (r1 - r0 + CH - 1) / CH;
+    if constexpr (PRE == 1) load_chunk<J, CH>(b1, W, K4, r0 + CH, r1, zero_row);
+    for (int c = 0; c < nch; c += 3) {
+        load_chunk<J, CH>(b2, W, K4, r0 + (c + 2) * CH, r1, zero_row);
+        chunk_step<J, CH, EPI>(b0, xv, r0 + c * CH, r1, red, rsel, e);
+        if (c + 1 >= nch) break;
+        load_chunk<J, CH>(b0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
+        chunk_step<J, CH, EPI>(b1, xv, r0 + (c + 1) * CH, r1, red, rsel, e);
+        if (c + 2 >= nch) break;
+        load_chunk<J, CH>(b1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
+        chunk_step<J, CH, EPI>(b2, xv, r0 + (c + 2) * CH, r1, red, rsel, e);
+    }
+}
+
+
+// Grid barrier, split so the caller can issue loads between arrival and wait.
+// Arrival: every wave waits for its own stores (vmcnt 0: the coherent stores have completed),
+// then thread 0 arrives on its group counter; the group's last arrival bumps the top counter.
+// bar[0] is the top counter, bar[8 * (1 + g)] the counter of group g (64 bytes apart).
+__device__ __forceinline__ void bar_arrive(unsigned long long* bar, int groups) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int gsize = (int)gridDim.x / groups;
+        const int g = (int)blockIdx.x % groups;
+        unsigned long long old = __hip_atomic_fetch_add(bar + 8 * (1 + g), 1ull, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+        if ((old + 1) % (unsigned long long)gsize == 0)
+            __hip_atomic_fetch_add(bar, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Wait until the top counter reaches `target`; false (uniformly over the workgroup) when the
+// wait gave up or another workgroup did.
+__device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long long target,
+                                         int* flag) {
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        long long n = 0;
+        while (__hip_atomic_load(a.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if ((++n & 127) == 0) {
+                if (__hip_atomic_load(a.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                    n > a.spin_limit) {
+                    __hip_atomic_store(a.abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = 0;
+                    break;
+                }
+            }
+        }
+        asm volatile("" ::: "memory");  // no load of the next phase moves above the wait
+        *flag = ok;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// xv = (x * rsqrt(mean(x^2) + eps)) * w for this thread's float4 columns t (K4 <= NT).
+// xv = (x * rsqrt(mean(x^2) + eps)) * w for this thread's float4 columns t (K4 <= NT).
+// x is read device-coherently unless it is a read-only row (the embedding); the raw x is
+// also kept in xs (LDS) so the residual add of the next phase reads it without a global load
+// (a load behind the prefetched weights would wait for all of them).
+__device__ __forceinline__ void norm_slice(const float* __restrict__ x, bool coherent,
+                                          const float* __restrict__ w, int K, float eps,
+                                          float* scratch, float* xs, float4 (&xv)[1]) {
+    const int t = threadIdx.x;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < K / 4) {
+        v = coherent ? ld_coh4(x + 4 * t) : ldg4(x + 4 * t);
+        *reinterpret_cast<float4*>(xs + 4 * t) = v;
+    }
+    float ss = block_sum(dot4(v, v), scratch);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    if (t < K / 4) {
+        float4 g = ldg4(w + 4 * t);
+        v = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z,
+                        (v.w * inv) * g.w);
+    }
+    xv[0] = v;
+}
+
+// Phase timestamp for the optional profile buffer (thread 0 of each workgroup).
+__device__ __forceinline__ void stamp(const PersistArgs& a, int it, int k, int which) {
+    if (a.prof && threadIdx.x == 0) {
+        const int nb = 5 * a.n_layers + 1;
+        a.prof[((size_t)(it * nb + k) * 4 + which) * gridDim.x + blockIdx.x] = wall_clock64();
+    }
+}
+
+constexpr int KSTRIDE = 68;  // LDS row stride of staged K rows: conflict-free 16-byte reads
+
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// Phase B1: the attention of query heads h = blockIdx.x, + gridDim.x, ... at position `pos`,
+// one workgroup per head, written to a.att (device-coherent).
+//
+// Per tile of 64 cached positions all 512 threads stage the K rows (padded to KSTRIDE) and V
+// rows of the head's KV group in LDS with coalesced device-coherent loads (one round trip;
+// the first tile also brings q, k and v of the current position).  Wavefront 0 then computes:
+// lane = position holds its K row, q[d] comes from lane d by readlane, an online softmax
+// (running max m, sum l; output o[lane = dim]) absorbs the tile, the PV weights are broadcast
+// the same way.  The current position comes last, from the rotated k / v; the workgroup of
+// the group's first query head appends those to the cache.  kv_s: [64][KSTRIDE] K |
+// [64][64] V | q, k, v [3][64].
+__device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int pos,
+                                                float* kv_s, int it, int kb) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int nq = a.n_heads, nkv = a.n_kv, grp = nq / nkv, S = a.max_seq;
+    const int64_t per_layer = (int64_t)nkv * S * 64;
+    float* kc = a.k_cache + l * per_layer;
+    float* vc = a.v_cache + l * per_layer;
+    float* ks = kv_s;
+    float* vs = ks + 64 * KSTRIDE;
+    float* cur = vs + 64 * 64;  // q | k | v of the current position
+    pos = __builtin_amdgcn_readfirstlane(pos);
+    // RoPE rotate-half, angle pos * theta^(-2j/64), j = lane mod 32
+    const int j = lane & 31;
+    const float inv_freq = 1.0f / powf(a.theta, (float)(2 * j) / 64.0f);
+    const float ang = (float)pos * inv_freq;
+    const float cs = cosf(ang), sn = sinf(ang);
+    for (int h = blockIdx.x; h < nq; h += gridDim.x) {
+        const int g = h / grp;
+        const float* kg = kc + (int64_t)g * S * 64;
+        const float* vg = vc + (int64_t)g * S * 64;
+        float qr = 0.0f, kr = 0.0f, vcur = 0.0f, o = 0.0f, m = -FLT_MAX, lsum = 0.0f;
+        for (int t0 = 0;; t0 += 64) {
+            const int nrows = min(64, pos - t0);  // cached rows in this tile (<= 0: none)
+            float4 k4[2], v4[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int f = t + NT * u, row = f >> 4, c4 = f & 15;
+                if (row < nrows) {
+                    k4[u] = ld_coh4(kg + (int64_t)(t0 + row) * 64 + c4 * 4);
+                    v4[u] = ld_coh4(vg + (int64_t)(t0 + row) * 64 + c4 * 4);
+                }
+            }
+            if (t0 == 0 && t < 48) {  // q_h, k_g, v_g: 3 x 16 float4
+                const int which = t >> 4, c4 = t & 15;
+                const int src = which == 0 ? h * 64 : which == 1 ? (nq + g) * 64 : (nq + nkv + g) * 64;
+                *reinterpret_cast<float4*>(cur + which * 64 + c4 * 4) = ld_coh4(a.qkv + src + c4 * 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int f = t + NT * u, row = f >> 4, c4 = f & 15;
+                if (row < nrows) {
+                    *reinterpret_cast<float4*>(ks + row * KSTRIDE + c4 * 4) = k4[u];
+                    *reinterpret_cast<float4*>(vs + row * 64 + c4 * 4) = v4[u];
+                }
+            }
+            __syncthreads();
+            if (t0 == 0) stamp(a, it, kb, 2);
+            if (wave == 0) {
+                if (t0 == 0) {
+                    const float q = cur[lane], k = cur[64 + lane];
+                    vcur = cur[128 + lane];
+                    const float qp = __shfl_xor(q, 32), kp = __shfl_xor(k, 32);
+                    qr = q * cs + (lane < 32 ? -qp : qp) * sn;
+                    kr = k * cs + (lane < 32 ? -kp : kp) * sn;
+                    if (h % grp == 0) {
+                        st_coh(kc + ((int64_t)g * S + pos) * 64 + lane, kr);
+                        st_coh(vc + ((int64_t)g * S + pos) * 64 + lane, vcur);
+                    }
+                }
+                if (nrows > 0) {
+                    const bool valid = lane < nrows;
+                    const float* krow = ks + lane * KSTRIDE;
+                    float sc = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * i);
+                        sc += lane_bcast(qr, 4 * i) * kk.x + lane_bcast(qr, 4 * i + 1) * kk.y +
+                              lane_bcast(qr, 4 * i + 2) * kk.z + lane_bcast(qr, 4 * i + 3) * kk.w;
+                    }
+                    sc = valid ? sc * 0.125f : -FLT_MAX;
+                    const float m_new = fmaxf(m, wave_max(sc));
+                    const float scale = expf(m - m_new);
+                    const float e = valid ? expf(sc - m_new) : 0.0f;
+                    lsum = lsum * scale + wave_sum(e);
+                    float acc = 0.0f;
+                    for (int i = 0; i < nrows; ++i) acc += lane_bcast(e, i) * vs[i * 64 + lane];
+                    o = o * scale + acc;
+                    m = m_new;
+                }
+            }
+            __syncthreads();  // the next tile's staging reuses ks / vs / cur
+            if (t0 + 64 >= pos) break;
+        }
+        if (wave == 0) {  // the current position, last in the sum
+            const float sc = wave_sum(qr * kr) * 0.125f;
+            const float m_new = fmaxf(m, sc);
+            const float scale = expf(m - m_new);
+            const float e = expf(sc - m_new);
+            st_coh(a.att + h * 64 + lane, (o * scale + e * vcur) / (lsum * scale + e));
+        }
+    }
+}
+
+template <int JF>
+__global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    constexpr int CHF = NB / JF;  // rows per chunk of the down projection
+    const int qd = a.n_heads * 64;
+    float* red = lds;                        // [2][NW][8]
+    float* scratch = lds + 2 * NW * 8;       // [NW] block sums
+    int* flag = reinterpret_cast<int*>(scratch + NW);
+    float* best_v = scratch + NW + 4;        // global argmax staging
+    int* best_i = reinterpret_cast<int*>(best_v + NW);
+    float* xs = lds + 256;                   // [hidden] raw x of the last norm (residual)
+    float* kv_s = xs + a.hidden;             // attention staging (attention_heads)
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int b = blockIdx.x, G = gridDim.x;
+    const int H = a.hidden, H4 = H / 4, F4 = a.ffn / 4, Q4 = qd / 4;
+    const int qkv_rows = (a.n_heads + 2 * a.n_kv) * 64;
+    int qa0, qa1, h0, h1, p0, p1, v0, v1;
+    part(qkv_rows, b, G, qa0, qa1);
+    part(H, b, G, h0, h1);
+    part(a.ffn, b, G, p0, p1);  // gate/up pairs
+    part(a.vocab, b, G, v0, v1);
+
+    float4 b0[NB], b1[NB], b2[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        b0[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        b1[i] = b0[i];
+        b2[i] = b0[i];
+    }
+    int rsel = 0;
+    unsigned long long target = a.bar_base;
+    // uniform over the workgroup; readfirstlane lets the compiler keep them (and everything
+    // derived from them) in scalar registers
+    int pos = __builtin_amdgcn_readfirstlane(a.st->pos);
+    int step = __builtin_amdgcn_readfirstlane(a.st->step);
+    int token = __builtin_amdgcn_readfirstlane(a.forced_token >= 0 ? a.forced_token : a.st->token);
+
+    load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
+    load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
+
+    for (int it = 0; it < a.n_tokens; ++it) {
+        const float* erow = a.embed + (int64_t)token * H;
+        int kb = 0;  // barrier index within the token (profile only)
+        for (int l = 0; l < a.n_layers; ++l) {
+            const PersistLayer L = a.layers[l];
+            const float* xin = l == 0 ? erow : a.x;
+            Epi e{};
+            // ---- A: qkv -------------------------------------------------------------------
+            {
+                float4 xv[1];
+                norm_slice(xin, l != 0, L.attn_norm, H, a.eps, scratch, xs, xv);
+                e.out = a.qkv;
+                stream_rows<1, 8, EPI_STORE>(L.wqkv, H4, qa0, qa1, xv, b0, b1, b2, red, rsel, e, a.zero_row);
+            }
+            stamp(a, it, kb, 0);
+            bar_arrive(a.bar, a.bar_groups);
+            load_chunk<1, 8>(b0, L.wo, Q4, h0, h1, a.zero_row);
+            load_chunk<1, 8>(b1, L.wo, Q4, h0 + 8, h1, a.zero_row);
+            target += a.bar_groups;
+            if (!bar_wait(a, target, flag)) return;
+            stamp(a, it, kb++, 1);
+            // ---- B1: attention, one workgroup per query head ------------------------------
+            attention_heads(a, l, pos, kv_s, it, kb);
+            stamp(a, it, kb, 0);
+            bar_arrive(a.bar, a.bar_groups);
+            target += a.bar_groups;
+            if (!bar_wait(a, target, flag)) return;
+            stamp(a, it, kb++, 1);
+            // ---- B2: Wo + residual --------------------------------------------------------
+            {
+                float4 xv[1];
+                xv[0] = t < Q4 ? ld_coh4(a.att + 4 * t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                e.out = a.x;
+                e.resid = xs;
+                stream_rows<1, 8, EPI_RESID>(L.wo, Q4, h0, h1, xv, b0, b1, b2, red, rsel, e,
+                                             a.zero_row);
+            }
+            stamp(a, it, kb, 0);
+            bar_arrive(a.bar, a.bar_groups);
+            load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
+            load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+            target += a.bar_groups;
+            if (!bar_wait(a, target, flag)) return;
+            stamp(a, it, kb++, 1);
+            // ---- C: gate/up + SwiGLU ------------------------------------------------------
+            {
+                float4 xv[1];
+                norm_slice(a.x, true, L.ffn_norm, H, a.eps, scratch, xs, xv);
+                e.out = a.act;
+                stream_rows<1, 8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, xv, b0, b1, b2, red,
+                                              rsel, e, a.zero_row);
+            }
+            stamp(a, it, kb, 0);
+            bar_arrive(a.bar, a.bar_groups);
+            load_chunk<JF, CHF>(b0, L.w_down, F4, h0, h1, a.zero_row);
+            load_chunk<JF, CHF>(b1, L.w_down, F4, h0 + CHF, h1, a.zero_row);
+            target += a.bar_groups;
+            if (!bar_wait(a, target, flag)) return;
+            stamp(a, it, kb++, 1);
+            // ---- D: down + residual -------------------------------------------------------
+            {
+                float4 xv[JF];
+#pragma unroll
+                for (int jj = 0; jj < JF; ++jj) {
+                    const int c = t + NT * jj;
+                    xv[jj] = c < F4 ? ld_coh4(a.act + 4 * c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+                e.out = a.x;
+                e.resid = xs;
+                stream_rows<JF, CHF, EPI_RESID>(L.w_down, F4, h0, h1, xv, b0, b1, b2, red, rsel,
+                                                e, a.zero_row);
+            }
+            stamp(a, it, kb, 0);
+            bar_arrive(a.bar, a.bar_groups);
+            {
+                const bool last = l + 1 == a.n_layers;
+                const float* Wn = last ? a.lm_head : a.layers[l + 1].wqkv;
+                const int n0 = last ? v0 : qa0, n1 = last ? v1 : qa1;
+                load_chunk<1, 8>(b0, Wn, H4, n0, n1, a.zero_row);
+                load_chunk<1, 8>(b1, Wn, H4, n0 + 8, n1, a.zero_row);
+            }
+            target += a.bar_groups;
+            if (!bar_wait(a, target, flag)) return;
+            stamp(a, it, kb++, 1);
+        }
+        // ---- E: lm_head + per-workgroup argmax ---------------------------------------------
+        {
+            float4 xv[1];
+            norm_slice(a.x, true, a.final_norm, H, a.eps, scratch, xs, xv);
+            Epi e{};
+            e.out = a.logits;
+            e.best = -FLT_MAX;
+            e.best_idx = 0x7fffffff;
+            stream_rows<1, 8, EPI_LOGITS>(a.lm_head, H4, v0, v1, xv, b0, b1, b2, red, rsel, e, a.zero_row);
+            if (t == 0) {
+                const unsigned long long packed =
+                    (unsigned long long)__float_as_uint(e.best) |
+                    ((unsigned long long)(unsigned)e.best_idx << 32);
+                __hip_atomic_store(reinterpret_cast<unsigned long long*>(a.cand + b), packed,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        stamp(a, it, kb, 0);
+        bar_arrive(a.bar, a.bar_groups);
+        // layer 0's first chunks for the next token (after the last token they go unused)
+        load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
+        load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
+        target += a.bar_groups;
+        if (!bar_wait(a, target, flag)) return;
+        stamp(a, it, kb++, 1);
+        // ---- F: global argmax (lowest index on ties), redundantly in every workgroup ------
+        {
+            float s = -FLT_MAX;
+            int idx = 0x7fffffff;
+            for (int i = t; i < G; i += NT) {
+                const unsigned long long packed =
+                    __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.cand + i),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float cv = __uint_as_float((unsigned)packed);
+                const int ci = (int)(unsigned)(packed >> 32);
+                if (cv > s || (cv == s && ci < idx)) { s = cv; idx = ci; }
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                float os = __shfl_xor(s, o);
+                int oi = __shfl_xor(idx, o);
+                if (os > s || (os == s && oi < idx)) { s = os; idx = oi; }
+            }
+            if (lane == 0) {
+                best_v[wave] = s;
+                best_i[wave] = idx;
+            }
+            __syncthreads();
+            s = best_v[0];
+            idx = best_i[0];
+            for (int w = 1; w < NW; ++w)
+                if (best_v[w] > s || (best_v[w] == s && best_i[w] < idx)) { s = best_v[w]; idx = best_i[w]; }
+            if (idx == 0x7fffffff) idx = 0;
+            __syncthreads();
+            if (b == 0 && t == 0) {
+                a.st->token = idx;
+                if (step < 4096) a.st->out_tokens[step] = idx;
+                a.st->step = step + 1;
+                a.st->pos = pos + 1;
+            }
+            token = __builtin_amdgcn_readfirstlane(idx);
+            ++step;
+            ++pos;
+        }
+    }
+}
+
+template <int JF>
+const void* kernel_for() {
+    return reinterpret_cast<const void*>(&decode_persistent_kernel<JF>);
+}
+
+const void* pick_kernel(int jf) {
+    switch (jf) {
+        case 1: return kernel_for<1>();
+        case 2: return kernel_for<2>();
+        case 3: return kernel_for<3>();
+        case 4: return kernel_for<4>();
+        default: return nullptr;
+    }
+}
+
+
+size_t lds_bytes(const PersistArgs& a) {
+    size_t floats = 256 + (size_t)a.hidden + 64 * KSTRIDE + 64 * 64 + 3 * 64;
+    return floats * sizeof(float);
+}
+
+}  // namespace
+
+namespace shp {
+
+int persist_plan(int device, PersistArgs* ap, int* grid, size_t* lds, std::string* why) {
+    const PersistArgs& a = *ap;
+    *grid = 0;
+    *lds = 0;
+    auto no = [&](const std::string& r) {
+        if (why) *why = r;
+        return SHP_OK;
+    };
+    const int qd = a.n_heads * 64;
+    if (a.hidden % 4 || a.hidden / 4 > NT) return no("hidden must be a multiple of 4, <= 2048");
+    if (qd / 4 > NT) return no("n_heads * 64 must be <= 2048");
+    if (a.ffn % 4) return no("ffn must be a multiple of 4");
+    const int jf = (a.ffn / 4 + NT - 1) / NT;
+    if (!pick_kernel(jf)) return no("ffn must be <= 8192");
+    if (a.n_kv <= 0 || a.n_heads % a.n_kv) return no("n_heads must be a multiple of n_kv");
+    if (a.max_seq <= 0) return no("max_seq");
+    int coop = 0, cus = 0;
+    SHP_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device));
+    SHP_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+    if (!coop) return no("device has no cooperative launch");
+    int max_lds = 0;
+    SHP_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+    const size_t bytes = lds_bytes(a);
+    if (bytes > (size_t)max_lds) return no("LDS for hidden + heads exceeds the device limit");
+    const void* k = pick_kernel(jf);
+    if (bytes > 64 * 1024)
+        SHP_HIP_CHECK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    int per_cu = 0;
+    SHP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, bytes));
+    if (per_cu < 1) return no("persistent kernel does not fit on a CU");
+    *grid = cus;  // one workgroup per CU
+    *lds = bytes;
+    return SHP_OK;
+}
+
+int persist_launch(hipStream_t s, const PersistArgs& a, int grid, size_t lds) {
+    const int jf = (a.ffn / 4 + NT - 1) / NT;
+    const void* k = pick_kernel(jf);
+    if (!k || grid <= 0) return fail(SHP_ERR_UNSUPPORTED, "persistent decode: not planned");
+    PersistArgs arg = a;
+    void* params[] = {&arg};
+    SHP_HIP_CHECK(hipLaunchCooperativeKernel(k, dim3(grid), dim3(NT), params, (unsigned)lds, s));
+    return SHP_OK;
+}
+
+}  // namespace shp

@@ -6,8 +6,10 @@
 // generated once in HBM, keys and values are cached, and a step is 5 launches per layer —
 // fused RMSNorm+QKV GEMV, RoPE+KV-append+attention, Wo GEMV with the residual add, fused
 // RMSNorm+gate/up GEMV with SiLU*up, down GEMV with the residual add — plus the final
-// RMSNorm+lm_head GEMV and an on-device argmax that feeds the next step.  The step is
-// captured once into a hipGraph; nothing returns to the host between tokens.
+// RMSNorm+lm_head GEMV and an on-device argmax that feeds the next step.  That step can run
+// eagerly or replayed from a hipGraph; the default engine instead runs a whole step or
+// decode call as one cooperative launch (kernels_decode_persist.hip).  Nothing returns to
+// the host between tokens in either form.
 #include <cmath>
 #include <vector>
 
@@ -32,10 +34,19 @@ struct Llama {
     std::vector<void*> allocs;
     double weight_bytes = 0.0;
     int host_pos = 0;
-    bool use_graph = true;
+    int engine = SHP_LLAMA_GRAPH;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     hipStream_t graph_stream = nullptr;
+
+    // persistent engine
+    PersistArgs pa{};
+    int p_grid = 0;
+    size_t p_lds = 0;
+    std::string p_why;
+    unsigned long long* bar = nullptr;
+    int* abort_flag = nullptr;
+    unsigned long long bar_top = 0;  // top barrier counter value after the last launch
 
     ~Llama() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -84,13 +95,51 @@ struct Llama {
         return rc;
     }
 
-    int step() {
-        if (host_pos >= cfg.max_seq)
+    int check_room(int n) {
+        if (host_pos + n > cfg.max_seq)
             return fail(SHP_ERR_SHAPE, "llama: KV cache full (position " +
-                                           std::to_string(host_pos) + " >= max_seq)");
-        if (host_pos >= 4096) return fail(SHP_ERR_SHAPE, "llama: token log full");
-        int rc;
-        if (!use_graph) {
+                                           std::to_string(host_pos + n - 1) + " >= max_seq)");
+        if (host_pos + n > 4096) return fail(SHP_ERR_SHAPE, "llama: token log full");
+        return SHP_OK;
+    }
+
+    // n tokens in one cooperative launch; forced >= 0 feeds that id as the first token.
+    // `prof` (optional) receives the phase timestamps (see PersistArgs::prof).
+    int persist_run(int n, int forced, unsigned long long* prof = nullptr) {
+        int rc = check_room(n);
+        if (rc) return rc;
+        PersistArgs a = pa;
+        a.bar_base = bar_top;
+        a.n_tokens = n;
+        a.forced_token = forced;
+        a.prof = prof;
+        rc = persist_launch(ctx->stream, a, p_grid, p_lds);
+        if (rc) return rc;
+        bar_top += (unsigned long long)n * persist_barriers_per_token(cfg.n_layers) *
+                   (unsigned long long)pa.bar_groups;
+        // a barrier wait that gave up makes every workgroup exit; report it and re-arm
+        int aborted = 0;
+        SHP_HIP_CHECK(hipMemcpyAsync(&aborted, abort_flag, sizeof(int), hipMemcpyDeviceToHost,
+                                     ctx->stream));
+        SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+        if (aborted) {
+            SHP_HIP_CHECK(hipMemsetAsync(bar, 0, kPersistBarSlots * sizeof(unsigned long long),
+                                         ctx->stream));
+            SHP_HIP_CHECK(hipMemsetAsync(abort_flag, 0, sizeof(int), ctx->stream));
+            SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+            bar_top = 0;
+            return fail(SHP_ERR_HIP, "llama: persistent decode grid barrier timed out; state "
+                                     "is undefined until reset");
+        }
+        host_pos += n;
+        return SHP_OK;
+    }
+
+    int step() {
+        int rc = check_room(1);
+        if (rc) return rc;
+        if (engine == SHP_LLAMA_PERSISTENT) return persist_run(1, -1);
+        if (engine == SHP_LLAMA_KERNELS) {
             rc = enqueue_step();
         } else {
             if (exec && graph_stream != ctx->stream) {
@@ -119,6 +168,64 @@ struct Llama {
         }
         if (!rc) ++host_pos;
         return rc;
+    }
+
+    int setup_persistent() {
+        pa = PersistArgs{};
+        std::vector<PersistLayer> hl;
+        for (const Layer& L : layers)
+            hl.push_back(PersistLayer{L.attn_norm, L.wqkv, L.wo, L.ffn_norm, L.w_gu, L.w_down});
+        PersistLayer* dl = nullptr;
+        SHP_HIP_CHECK(hipMalloc((void**)&dl, hl.size() * sizeof(PersistLayer)));
+        allocs.push_back(dl);
+        SHP_HIP_CHECK(hipMemcpy(dl, hl.data(), hl.size() * sizeof(PersistLayer),
+                                hipMemcpyHostToDevice));
+        const int qd = cfg.n_heads * cfg.head_dim;
+        const uint64_t zrow = (uint64_t)std::max(std::max(cfg.hidden, qd), cfg.ffn);
+        float* zero = nullptr;
+        int rc = alloc(&zero, zrow);
+        if (rc) return rc;
+        SHP_HIP_CHECK(hipMemset(zero, 0, zrow * sizeof(float)));
+        SHP_HIP_CHECK(hipMalloc((void**)&bar, kPersistBarSlots * sizeof(unsigned long long)));
+        allocs.push_back(bar);
+        SHP_HIP_CHECK(hipMemset(bar, 0, kPersistBarSlots * sizeof(unsigned long long)));
+        SHP_HIP_CHECK(hipMalloc((void**)&abort_flag, sizeof(int)));
+        allocs.push_back(abort_flag);
+        SHP_HIP_CHECK(hipMemset(abort_flag, 0, sizeof(int)));
+        pa.layers = dl;
+        pa.embed = embed;
+        pa.final_norm = final_norm;
+        pa.lm_head = lm_head;
+        pa.k_cache = k_cache;
+        pa.v_cache = v_cache;
+        pa.x = x;
+        pa.qkv = qkv;
+        pa.att = att;
+        pa.act = act;
+        pa.logits = logits;
+        pa.zero_row = zero;
+        pa.st = st;
+        pa.bar = bar;
+        pa.abort_flag = abort_flag;
+        pa.spin_limit = 1ll << 22;  // ~1 us per poll: a wait gives up after seconds
+        pa.n_layers = cfg.n_layers;
+        pa.hidden = cfg.hidden;
+        pa.n_heads = cfg.n_heads;
+        pa.n_kv = cfg.n_kv_heads;
+        pa.ffn = cfg.ffn;
+        pa.vocab = cfg.vocab;
+        pa.max_seq = cfg.max_seq;
+        pa.eps = cfg.rms_eps;
+        pa.theta = cfg.rope_theta;
+        rc = persist_plan(ctx->device, &pa, &p_grid, &p_lds, &p_why);
+        if (rc) return rc;
+        if (p_grid <= 0) return SHP_OK;  // unsupported: p_why says why
+        ArgmaxCand* cand = nullptr;
+        SHP_HIP_CHECK(hipMalloc((void**)&cand, (size_t)p_grid * sizeof(ArgmaxCand)));
+        allocs.push_back(cand);
+        pa.cand = cand;
+        pa.bar_groups = persist_bar_groups(p_grid);
+        return SHP_OK;
     }
 
     int reset() {
@@ -183,6 +290,8 @@ int shp_llama_create(shp_ctx* ctx, const shp_llama_config* cfg, uint64_t seed, s
         else lm->allocs.push_back(lm->st);
     }
     if (!rc) rc = lm->reset();
+    if (!rc) rc = lm->setup_persistent();
+    if (!rc && lm->p_grid > 0) lm->engine = SHP_LLAMA_PERSISTENT;
     if (!rc) {
         hipError_t e = hipStreamSynchronize(lm->ctx->stream);
         if (e != hipSuccess) rc = fail(SHP_ERR_HIP, hipGetErrorString(e));
@@ -211,6 +320,7 @@ int shp_llama_step(shp_llama* p, int32_t token) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_step: null");
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (token < 0 || token >= lm->cfg.vocab) return fail(SHP_ERR_SHAPE, "shp_llama_step: token id");
+    if (lm->engine == SHP_LLAMA_PERSISTENT) return lm->persist_run(1, token);
     int rc = shp::set_token_launch(lm->ctx->stream, lm->st, token);
     return rc ? rc : lm->step();
 }
@@ -218,6 +328,9 @@ int shp_llama_step(shp_llama* p, int32_t token) {
 int shp_llama_decode(shp_llama* p, int32_t n_steps) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_decode: null");
     Llama* lm = reinterpret_cast<Llama*>(p);
+    if (n_steps < 0) return fail(SHP_ERR_INVALID, "shp_llama_decode: n_steps < 0");
+    if (n_steps == 0) return SHP_OK;
+    if (lm->engine == SHP_LLAMA_PERSISTENT) return lm->persist_run(n_steps, -1);
     for (int i = 0; i < n_steps; ++i) {
         int rc = lm->step();
         if (rc) return rc;
@@ -268,7 +381,50 @@ int shp_llama_generate(shp_llama* p, const int32_t* prompt, int32_t n_prompt, in
 
 int shp_llama_use_graph(shp_llama* p, int enable) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_use_graph: null");
-    reinterpret_cast<Llama*>(p)->use_graph = enable != 0;
+    reinterpret_cast<Llama*>(p)->engine = enable ? SHP_LLAMA_GRAPH : SHP_LLAMA_KERNELS;
+    return SHP_OK;
+}
+
+int shp_llama_set_engine(shp_llama* p, int engine) {
+    if (!p) return fail(SHP_ERR_INVALID, "shp_llama_set_engine: null");
+    Llama* lm = reinterpret_cast<Llama*>(p);
+    if (engine != SHP_LLAMA_KERNELS && engine != SHP_LLAMA_GRAPH && engine != SHP_LLAMA_PERSISTENT)
+        return fail(SHP_ERR_INVALID, "shp_llama_set_engine: unknown engine");
+    if (engine == SHP_LLAMA_PERSISTENT && lm->p_grid <= 0)
+        return fail(SHP_ERR_UNSUPPORTED, "shp_llama_set_engine: persistent engine unavailable: " +
+                                             lm->p_why);
+    lm->engine = engine;
+    return SHP_OK;
+}
+
+// Internal profiling hook (not part of include/spirv_hip.h): decodes n tokens with the
+// persistent engine and copies the phase timestamps to host_out, which must hold
+// n * (5 * n_layers + 1) * 4 * grid values; *grid receives the workgroup count.
+int shp_llama_profile_persistent(shp_llama* p, int32_t n, unsigned long long* host_out,
+                                 uint64_t cap, int32_t* grid) {
+    if (!p || !host_out || !grid || n <= 0)
+        return fail(SHP_ERR_INVALID, "shp_llama_profile_persistent: bad arguments");
+    Llama* lm = reinterpret_cast<Llama*>(p);
+    if (lm->p_grid <= 0) return fail(SHP_ERR_UNSUPPORTED, "persistent engine unavailable");
+    const uint64_t need = (uint64_t)n * shp::persist_barriers_per_token(lm->cfg.n_layers) * 4 *
+                          (uint64_t)lm->p_grid;
+    if (cap < need) return fail(SHP_ERR_INVALID, "shp_llama_profile_persistent: buffer too small");
+    unsigned long long* d = nullptr;
+    SHP_HIP_CHECK(hipMalloc((void**)&d, need * sizeof(unsigned long long)));
+    int rc = lm->persist_run(n, -1, d);
+    if (!rc) {
+        hipError_t e = hipMemcpy(host_out, d, need * sizeof(unsigned long long),
+                                 hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = fail(SHP_ERR_HIP, hipGetErrorString(e));
+    }
+    (void)hipFree(d);
+    *grid = lm->p_grid;
+    return rc;
+}
+
+int shp_llama_engine(shp_llama* p, int* engine) {
+    if (!p || !engine) return fail(SHP_ERR_INVALID, "shp_llama_engine: null");
+    *engine = reinterpret_cast<Llama*>(p)->engine;
     return SHP_OK;
 }
 

@@ -146,6 +146,19 @@ class Llama:
     def use_graph(self, enable: bool):
         check(lib().shp_llama_use_graph(self.handle, int(enable)), "shp_llama_use_graph")
 
+    ENGINES = {"kernels": 0, "graph": 1, "persistent": 2}
+
+    def set_engine(self, name: str):
+        """'kernels' (eager per-op launches), 'graph' (per-token hipGraph) or 'persistent'
+        (one cooperative launch per step/decode call; the default where supported)."""
+        check(lib().shp_llama_set_engine(self.handle, self.ENGINES[name]), "shp_llama_set_engine")
+
+    @property
+    def engine(self) -> str:
+        e = C.c_int()
+        check(lib().shp_llama_engine(self.handle, C.byref(e)), "shp_llama_engine")
+        return {v: k for k, v in self.ENGINES.items()}[e.value]
+
     def step(self, token: int):
         check(lib().shp_llama_step(self.handle, int(token)), "shp_llama_step")
 

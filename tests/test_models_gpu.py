@@ -114,13 +114,15 @@ SMALL = dict(n_layers=2, hidden=256, n_heads=8, n_kv_heads=2, head_dim=64, ffn=5
              max_seq=64, rms_eps=1e-5, rope_theta=10000.0)
 
 
-@pytest.mark.parametrize("graph", [False, True])
-def test_llama_small_tokens_and_logits(ctx, orc, graph):
+@pytest.mark.parametrize("engine", ["kernels", "graph", "persistent"])
+def test_llama_small_tokens_and_logits(ctx, orc, engine):
     from spirv_inference_amd.models import Llama
     rng = np.random.default_rng(3)
     prompt = [int(t) for t in rng.integers(0, SMALL["vocab"], 12)]
+    print(f"[llama small] engine={engine}", flush=True)
     with Llama(ctx, seed=5, **SMALL) as lm:
-        lm.use_graph(graph)
+        lm.set_engine(engine)
+        assert lm.engine == engine
         lm.reset()
         gpu_logits = []
         for t in prompt:
@@ -151,12 +153,36 @@ def test_llama_kv_cache_matches_full_recompute(ctx, orc):
             assert_close(step_logits[pos], full[pos], 1e-5, 1e-4, f"pos {pos}")
 
 
+def test_llama_small_multi_token_persistent_call(ctx, orc):
+    """One persistent launch decoding several tokens (the prompt fed one launch per id)
+    equals the oracle's token-by-token decode; mixing engines mid-sequence is consistent."""
+    from spirv_inference_amd.models import Llama
+    rng = np.random.default_rng(7)
+    prompt = [int(t) for t in rng.integers(0, SMALL["vocab"], 9)]
+    with Llama(ctx, seed=8, **SMALL) as lm:
+        lm.set_engine("persistent")
+        lm.reset()
+        for t in prompt:
+            lm.step(t)
+        lm.decode(6)                      # one launch, 6 tokens
+        lm.set_engine("graph")
+        lm.decode(2)                      # continue on the per-op engine
+        lm.set_engine("persistent")
+        lm.decode(3)
+        got = lm.tokens()[len(prompt) - 1:]
+        want, logits, _ = oracle_decode(orc, lm, SMALL, prompt, 12)
+        assert got == want
+        assert_close(lm.logits(), logits[-1], 1e-4, 1e-4, "final logits")
+
+
 def test_tinyllama_full_greedy_tokens(ctx, orc):
-    """TinyLlama-1.1B shape, 32 seeded prompt ids, 20 greedy tokens: identical to the oracle."""
+    """TinyLlama-1.1B shape, 32 seeded prompt ids, 20 greedy tokens: identical to the oracle
+    (default engine: persistent), and the per-op graph engine gives the same tokens."""
     from spirv_inference_amd.models import TINYLLAMA, Llama
     rng = np.random.default_rng(3)
     prompt = [int(t) for t in rng.integers(0, 32000, 32)]
     with Llama(ctx, seed=2) as lm:
+        print(f"[tinyllama] engine={lm.engine}", flush=True)
         got = lm.generate(prompt, 20)
         gpu_last = lm.logits()
         want, logits, _ = oracle_decode(orc, lm, TINYLLAMA, prompt, 20)
@@ -165,3 +191,6 @@ def test_tinyllama_full_greedy_tokens(ctx, orc):
         print(f"[tinyllama] gpu={got}\n[tinyllama] cpu={want_kept}")
         assert got == want_kept
         assert_close(gpu_last, logits[-1], 1e-4, 1e-4, "final logits")
+        lm.set_engine("graph")
+        assert lm.generate(prompt, 20) == got
+        assert_close(lm.logits(), gpu_last, 1e-4, 1e-4, "graph vs persistent logits")
