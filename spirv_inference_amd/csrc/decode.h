@@ -67,27 +67,25 @@ struct PersistArgs {
     ArgmaxCand* cand;  // [grid] per-workgroup argmax of its logits rows
     const float* zero_row;  // >= max(hidden, n_heads * 64, ffn) zeros (padding-row loads)
     DecodeState* st;
-    unsigned long long* bar;  // barrier counters: [0] top, [8 * (1 + g)] group g (monotonic)
-    int* abort_flag;          // set when a barrier wait exceeds spin_limit
-    unsigned long long bar_base;  // top counter value when this launch starts
-    int bar_groups;               // arrival groups; the top counter gains this per barrier
+    unsigned long long* flags;  // barrier epoch flag of workgroup b at flags[8 * b] (monotonic)
+    int* abort_flag;            // set when a barrier wait exceeds spin_limit
+    unsigned long long bar_base;  // barriers completed before this launch (epoch base)
     long long spin_limit;         // polls of the counter before a wait gives up
     int n_layers, hidden, n_heads, n_kv, ffn, vocab, max_seq;
     float eps, theta;
     int n_tokens;      // tokens decoded by this launch
     int forced_token;  // >= 0: the first token fed (a prompt id); < 0: state.token
     // Optional phase timestamps (100 MHz wall clock), null when not profiling:
-    // prof[((token * barriers_per_token + k) * 4 + slot) * grid + workgroup], slot 0 arrival
-    // at barrier k, 1 its pass; in the attention phase 2 = first tile staged.
+    // prof[((token * barriers_per_token + k) * 16 + slot) * grid + workgroup], slot 0 arrival
+    // at barrier k, 1 its pass; in the attention phase 2 = first tile staged; in the gate/up
+    // phase 3 = vector normalised, 4 + c = chunk c done.
     unsigned long long* prof;
 };
 
 // Grid barriers one token costs: five per layer and one before the global argmax.
 inline int persist_barriers_per_token(int n_layers) { return 5 * n_layers + 1; }
-// Arrival groups of the two-level barrier for a grid of `grid` workgroups.
-inline int persist_bar_groups(int grid) { return grid % 16 == 0 ? 16 : 1; }
-// unsigned long long slots the barrier counters occupy.
-constexpr int kPersistBarSlots = 8 * 17;
+// unsigned long long slots of the barrier flags of a grid of `grid` workgroups.
+inline int persist_flag_slots(int grid) { return 8 * grid; }
 
 // Checks that the persistent kernel supports this shape and that the device can keep one
 // workgroup per CU resident.  On success *grid > 0 and *lds is the dynamic LDS size;

@@ -23,14 +23,16 @@
 // argmax, then F the global argmax (every workgroup reduces the candidates itself).
 // Layer 0 reads the embedding row directly, so no barrier is needed between tokens.
 //
-// Weight rows are streamed with 16-byte non-temporal loads, three chunks deep per thread.
+// Weight rows are streamed with 16-byte non-temporal loads, up to three chunks (64 KB each per
+// CU) ahead of the arithmetic, on a schedule that keeps each CU's load pipe (~30 GB/s, ~64 KB
+// in flight) busy through the short latency-bound phases (see the layer loop).
 //
 // Cross-workgroup data (qkv, x, act, the KV cache rows, the argmax candidates) is written and
 // read with agent-scope relaxed atomics, i.e. stores and loads that go to the device-coherent
 // level instead of the per-XCD L2.  A barrier is then only: every wave waits for its stores
-// to complete, one arrival per workgroup on a group counter (16 groups), the last arrival of
-// a group bumps the top counter, and thread 0 polls the top counter.  No L2 write-back or
-// invalidate is needed, which is what makes a barrier ~3 us instead of ~10-30 us on MI355X.
+// to complete, each workgroup stores the barrier's epoch into its own flag, and four
+// wavefronts poll the flags.  No L2 write-back or invalidate is needed, which is what makes a
+// barrier ~2.5 us instead of ~10-30 us with release/acquire fences on MI355X.
 // Every wait is bounded (spin_limit polls); on expiry the workgroup raises abort_flag and
 // every workgroup exits, so the grid always drains.
 #include <cfloat>
@@ -130,8 +132,9 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 // Chunk of CH rows [rc, rc + CH) of a row-major [rows][K4] float4 matrix: thread t holds
 // columns t + NT*j (j < J) of each row.  Every slot is loaded unconditionally (a branch would
 // make the register allocator copy the previous chunk's values, which waits for their loads):
-// rows >= r1 read the zero row instead, columns >= K4 are clamped to the last column (the
-// vector slice is zero there).  Row bases are uniform, per-thread offsets 32-bit.
+// rows >= r1 read the zero row instead (a few KB that stay in L2), columns >= K4 are clamped
+// to the last column (the vector slice is zero there).  Row bases are uniform, per-thread
+// offsets 32-bit.
 template <int J, int CH>
 __device__ __forceinline__ void load_chunk(float4 (&b)[NB], const float* __restrict__ W, int K4,
                                            int rc, int r1, const float* zero_row) {
@@ -179,11 +182,19 @@ __device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 struct Epi {
+    unsigned long long* prof;  // profile only (null otherwise)
+    int prof_it, prof_kb, prof_nb;
     float* out;
     const float* resid;  // EPI_RESID: LDS copy of the vector added per row
     float best;          // EPI_LOGITS: running max / index (thread 0)
     int best_idx;
 };
+
+__device__ __forceinline__ void stamp_in(const Epi& e, int which) {
+    if (e.prof && threadIdx.x == 0 && which < 16)
+        e.prof[((size_t)(e.prof_it * e.prof_nb + e.prof_kb) * 16 + which) * gridDim.x +
+               blockIdx.x] = wall_clock64();
+}
 
 // One chunk: partial dot products of the CH rows in `b`, the workgroup reduction, and the
 // epilogue for rows rc..rc+CH-1.  `red` is [2][NW][8] floats, alternated by `rsel`.
@@ -275,62 +286,95 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4,
 }
 
 
-// Grid barrier, split so the caller can issue loads between arrival and wait.
-// Arrival: every wave waits for its own stores (vmcnt 0: the coherent stores have completed),
-// then thread 0 arrives on its group counter; the group's last arrival bumps the top counter.
-// bar[0] is the top counter, bar[8 * (1 + g)] the counter of group g (64 bytes apart).
-__device__ __forceinline__ void bar_arrive(unsigned long long* bar, int groups) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int gsize = (int)gridDim.x / groups;
-        const int g = (int)blockIdx.x % groups;
-        unsigned long long old = __hip_atomic_fetch_add(bar + 8 * (1 + g), 1ull, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT);
-        if ((old + 1) % (unsigned long long)gsize == 0)
-            __hip_atomic_fetch_add(bar, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// As stream_rows, with chunks 0, 1 and 2 already issued into c0, c1 and c2; the load of
+// chunk c+3 is issued as soon as chunk c has been consumed.
+template <int J, int CH, int EPI>
+__device__ __forceinline__ void stream_rows3(const float* __restrict__ W, int K4, int r0, int r1,
+                                             const float4 (&xv)[J], float4 (&c0)[NB],
+                                             float4 (&c1)[NB], float4 (&c2)[NB], float* red,
+                                             int& rsel, Epi& e, const float* zero_row) {
+    const int nch = (r1 - r0 + CH - 1) / CH;
+    for (int c = 0; c < nch; c += 3) {
+        chunk_step<J, CH, EPI>(c0, xv, r0 + c * CH, r1, red, rsel, e);
+        stamp_in(e, 4 + c);
+        load_chunk<J, CH>(c0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
+        if (c + 1 >= nch) break;
+        chunk_step<J, CH, EPI>(c1, xv, r0 + (c + 1) * CH, r1, red, rsel, e);
+        stamp_in(e, 5 + c);
+        load_chunk<J, CH>(c1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
+        if (c + 2 >= nch) break;
+        chunk_step<J, CH, EPI>(c2, xv, r0 + (c + 2) * CH, r1, red, rsel, e);
+        stamp_in(e, 6 + c);
+        load_chunk<J, CH>(c2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
     }
 }
 
-// Wait until the top counter reaches `target`; false (uniformly over the workgroup) when the
-// wait gave up or another workgroup did.
-__device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long long target,
-                                         int* flag) {
-    if (threadIdx.x == 0) {
+// Grid barrier, split so the caller can issue loads between arrival and wait.
+// Arrival: every wave waits for its own stores (vmcnt 0: the coherent stores have completed),
+// then thread 0 stores the barrier's epoch into the workgroup's flag (64 bytes apart; no
+// atomics, so no contention).  Wait: wavefronts 0 .. ceil(grid/64)-1 poll 64 flags each until
+// all have reached the epoch.  On MI355X this takes ~2.4 us against ~3.7 us for a two-level
+// atomic counter.
+__device__ __forceinline__ void bar_arrive(unsigned long long* flags, unsigned long long epoch) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_store((SHP_GLOBAL unsigned long long*)(flags + 8 * blockIdx.x), epoch,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until every workgroup's flag holds `epoch`; false (uniformly over the workgroup) when
+// a wait gave up or another workgroup did.  okw: NW ints of LDS.
+__device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long long epoch,
+                                         int* okw) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int G = gridDim.x;
+    if (wave * 64 < G) {
+        const int f = wave * 64 + lane;
         int ok = 1;
         long long n = 0;
-        while (__hip_atomic_load(a.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        while (true) {
+            const unsigned long long v =
+                f < G ? __hip_atomic_load((SHP_GLOBAL unsigned long long*)(a.flags + 8 * f),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : ~0ull;
+            if (__all(v >= epoch)) break;
             __builtin_amdgcn_s_sleep(1);
             if ((++n & 127) == 0) {
-                if (__hip_atomic_load(a.abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                if (__hip_atomic_load((SHP_GLOBAL int*)a.abort_flag, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) != 0 ||
                     n > a.spin_limit) {
-                    __hip_atomic_store(a.abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0)
+                        __hip_atomic_store((SHP_GLOBAL int*)a.abort_flag, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                     ok = 0;
                     break;
                 }
             }
         }
         asm volatile("" ::: "memory");  // no load of the next phase moves above the wait
-        *flag = ok;
+        if (lane == 0) okw[wave] = ok;
     }
     __syncthreads();
-    return *flag != 0;
+    int ok = 1;
+    for (int w = 0; w * 64 < G; ++w) ok &= okw[w];
+    return ok != 0;
 }
 
-// xv = (x * rsqrt(mean(x^2) + eps)) * w for this thread's float4 columns t (K4 <= NT).
-// xv = (x * rsqrt(mean(x^2) + eps)) * w for this thread's float4 columns t (K4 <= NT).
-// x is read device-coherently unless it is a read-only row (the embedding); the raw x is
-// also kept in xs (LDS) so the residual add of the next phase reads it without a global load
-// (a load behind the prefetched weights would wait for all of them).
-__device__ __forceinline__ void norm_slice(const float* __restrict__ x, bool coherent,
-                                          const float* __restrict__ w, int K, float eps,
-                                          float* scratch, float* xs, float4 (&xv)[1]) {
+// RMSNorm of the vector slice, in two steps so weight loads can be issued between them:
+// norm_load issues this thread's float4 of x (device-coherent unless it is a read-only row,
+// the embedding) and keeps it in xs (LDS) for the residual add of the next phase;
+// norm_finish forms xv = (x * rsqrt(mean(x^2) + eps)) * w.  K4 <= NT.
+__device__ __forceinline__ float4 norm_load(const float* __restrict__ x, bool coherent, int K) {
     const int t = threadIdx.x;
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (t < K / 4) {
-        v = coherent ? ld_coh4(x + 4 * t) : ldg4(x + 4 * t);
-        *reinterpret_cast<float4*>(xs + 4 * t) = v;
-    }
+    if (t < K / 4) v = coherent ? ld_coh4(x + 4 * t) : ldg4(x + 4 * t);
+    return v;
+}
+__device__ __forceinline__ void norm_finish(float4 v, const float* __restrict__ w, int K, float eps,
+                                           float* scratch, float* xs, float4 (&xv)[1]) {
+    const int t = threadIdx.x;
+    if (t < K / 4) *reinterpret_cast<float4*>(xs + 4 * t) = v;
     float ss = block_sum(dot4(v, v), scratch);
     const float inv = 1.0f / sqrtf(ss / (float)K + eps);
     if (t < K / 4) {
@@ -345,7 +389,7 @@ __device__ __forceinline__ void norm_slice(const float* __restrict__ x, bool coh
 __device__ __forceinline__ void stamp(const PersistArgs& a, int it, int k, int which) {
     if (a.prof && threadIdx.x == 0) {
         const int nb = 5 * a.n_layers + 1;
-        a.prof[((size_t)(it * nb + k) * 4 + which) * gridDim.x + blockIdx.x] = wall_clock64();
+        a.prof[((size_t)(it * nb + k) * 16 + which) * gridDim.x + blockIdx.x] = wall_clock64();
     }
 }
 
@@ -362,10 +406,10 @@ __device__ __forceinline__ float lane_bcast(float v, int src) {
 // rows of the head's KV group in LDS with coalesced device-coherent loads (one round trip;
 // the first tile also brings q, k and v of the current position).  Wavefront 0 then computes:
 // lane = position holds its K row, q[d] comes from lane d by readlane, an online softmax
-// (running max m, sum l; output o[lane = dim]) absorbs the tile, the PV weights are broadcast
-// the same way.  The current position comes last, from the rotated k / v; the workgroup of
-// the group's first query head appends those to the cache.  kv_s: [64][KSTRIDE] K |
-// [64][64] V | q, k, v [3][64].
+// (running max m, sum l; output o[lane = dim]) absorbs the tile, and the weights are shared
+// through LDS to all 8 wavefronts, which split the PV sum.  The current position comes last,
+// from the rotated k / v; the workgroup of the group's first query head appends those to
+// the cache.  kv_s: [64][KSTRIDE] K | [64][64] V | q, k, v [3][64] | p [64] | PV [NW][64].
 __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int pos,
                                                 float* kv_s, int it, int kb) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -376,6 +420,8 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
     float* ks = kv_s;
     float* vs = ks + 64 * KSTRIDE;
     float* cur = vs + 64 * 64;  // q | k | v of the current position
+    float* pe = cur + 3 * 64;   // [64] softmax weights of the tile
+    float* po = pe + 64;        // [NW][64] PV partial sums
     pos = __builtin_amdgcn_readfirstlane(pos);
     // RoPE rotate-half, angle pos * theta^(-2j/64), j = lane mod 32
     const int j = lane & 31;
@@ -413,6 +459,7 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
             }
             __syncthreads();
             if (t0 == 0) stamp(a, it, kb, 2);
+            float scale = 1.0f;
             if (wave == 0) {
                 if (t0 == 0) {
                     const float q = cur[lane], k = cur[64 + lane];
@@ -437,13 +484,29 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
                     }
                     sc = valid ? sc * 0.125f : -FLT_MAX;
                     const float m_new = fmaxf(m, wave_max(sc));
-                    const float scale = expf(m - m_new);
+                    scale = expf(m - m_new);
                     const float e = valid ? expf(sc - m_new) : 0.0f;
                     lsum = lsum * scale + wave_sum(e);
-                    float acc = 0.0f;
-                    for (int i = 0; i < nrows; ++i) acc += lane_bcast(e, i) * vs[i * 64 + lane];
-                    o = o * scale + acc;
                     m = m_new;
+                    pe[lane] = e;
+                }
+            }
+            if (nrows > 0) {
+                __syncthreads();
+                // PV partial sums: wavefront w takes positions w*8 .. w*8+7 of the tile
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int tt = wave * 8 + i;
+                    if (tt < nrows) acc += pe[tt] * vs[tt * 64 + lane];
+                }
+                po[wave * 64 + lane] = acc;
+                __syncthreads();
+                if (wave == 0) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) sum += po[w * 64 + lane];
+                    o = o * scale + sum;
                 }
             }
             __syncthreads();  // the next tile's staging reuses ks / vs / cur
@@ -466,7 +529,7 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
     const int qd = a.n_heads * 64;
     float* red = lds;                        // [2][NW][8]
     float* scratch = lds + 2 * NW * 8;       // [NW] block sums
-    int* flag = reinterpret_cast<int*>(scratch + NW);
+    int* okw = reinterpret_cast<int*>(lds + 160);  // [NW] barrier wait results
     float* best_v = scratch + NW + 4;        // global argmax staging
     int* best_i = reinterpret_cast<int*>(best_v + NW);
     float* xs = lds + 256;                   // [hidden] raw x of the last norm (residual)
@@ -497,9 +560,10 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
     int step = __builtin_amdgcn_readfirstlane(a.st->step);
     int token = __builtin_amdgcn_readfirstlane(a.forced_token >= 0 ? a.forced_token : a.st->token);
 
+
+    const bool attn_wg = b < a.n_heads;  // this workgroup computes an attention head
     load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
     load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
-
     for (int it = 0; it < a.n_tokens; ++it) {
         const float* erow = a.embed + (int64_t)token * H;
         int kb = 0;  // barrier index within the token (profile only)
@@ -507,57 +571,71 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             const PersistLayer L = a.layers[l];
             const float* xin = l == 0 ? erow : a.x;
             Epi e{};
-            // ---- A: qkv -------------------------------------------------------------------
+            // Prefetch schedule.  A CU streams ~30 GB/s with ~64 KB in flight; loads return in
+            // issue order, so a load issued before a barrier delays that barrier's poll.  The
+            // pipe is kept busy through the short phases: qkv chunks 0-1 at the previous
+            // barrier, Wo at the start of the qkv phase, gate/up 0-1 at the qkv barrier (or,
+            // for the workgroups that compute attention, after it), gate/up 2 at the Wo
+            // barrier, down 0-1 at the gate/up barrier.
+            // ---- A: qkv (at most two chunks, both resident) -------------------------------
             {
+                float4 xr = norm_load(xin, l != 0, H);
+                load_chunk<1, 8>(b2, L.wo, Q4, h0, h1, a.zero_row);
                 float4 xv[1];
-                norm_slice(xin, l != 0, L.attn_norm, H, a.eps, scratch, xs, xv);
+                norm_finish(xr, L.attn_norm, H, a.eps, scratch, xs, xv);
                 e.out = a.qkv;
-                stream_rows<1, 8, EPI_STORE>(L.wqkv, H4, qa0, qa1, xv, b0, b1, b2, red, rsel, e, a.zero_row);
+                chunk_step<1, 8, EPI_STORE>(b0, xv, qa0, qa1, red, rsel, e);
+                chunk_step<1, 8, EPI_STORE>(b1, xv, qa0 + 8, qa1, red, rsel, e);
             }
             stamp(a, it, kb, 0);
-            bar_arrive(a.bar, a.bar_groups);
-            load_chunk<1, 8>(b0, L.wo, Q4, h0, h1, a.zero_row);
-            load_chunk<1, 8>(b1, L.wo, Q4, h0 + 8, h1, a.zero_row);
-            target += a.bar_groups;
-            if (!bar_wait(a, target, flag)) return;
+            bar_arrive(a.flags, target + 1);
+            if (!attn_wg) {
+                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
+                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+            }
+            target += 1;
+            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- B1: attention, one workgroup per query head ------------------------------
             attention_heads(a, l, pos, kv_s, it, kb);
             stamp(a, it, kb, 0);
-            bar_arrive(a.bar, a.bar_groups);
-            target += a.bar_groups;
-            if (!bar_wait(a, target, flag)) return;
+            bar_arrive(a.flags, target + 1);
+            if (attn_wg) {
+                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
+                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+            }
+            target += 1;
+            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
-            // ---- B2: Wo + residual --------------------------------------------------------
+            // ---- B2: Wo + residual (one chunk: h1 - h0 <= 8) ------------------------------
             {
                 float4 xv[1];
                 xv[0] = t < Q4 ? ld_coh4(a.att + 4 * t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 e.out = a.x;
                 e.resid = xs;
-                stream_rows<1, 8, EPI_RESID>(L.wo, Q4, h0, h1, xv, b0, b1, b2, red, rsel, e,
-                                             a.zero_row);
+                chunk_step<1, 8, EPI_RESID>(b2, xv, h0, h1, red, rsel, e);
             }
             stamp(a, it, kb, 0);
-            bar_arrive(a.bar, a.bar_groups);
-            load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
-            load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
-            target += a.bar_groups;
-            if (!bar_wait(a, target, flag)) return;
+            bar_arrive(a.flags, target + 1);
+            load_chunk<1, 8>(b2, L.w_gu, H4, 2 * p0 + 16, 2 * p1, a.zero_row);
+            target += 1;
+            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- C: gate/up + SwiGLU ------------------------------------------------------
             {
+                float4 xr = norm_load(a.x, true, H);
                 float4 xv[1];
-                norm_slice(a.x, true, L.ffn_norm, H, a.eps, scratch, xs, xv);
+                norm_finish(xr, L.ffn_norm, H, a.eps, scratch, xs, xv);
                 e.out = a.act;
-                stream_rows<1, 8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, xv, b0, b1, b2, red,
-                                              rsel, e, a.zero_row);
+                stream_rows3<1, 8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, xv, b0, b1, b2, red,
+                                               rsel, e, a.zero_row);
             }
             stamp(a, it, kb, 0);
-            bar_arrive(a.bar, a.bar_groups);
+            bar_arrive(a.flags, target + 1);
             load_chunk<JF, CHF>(b0, L.w_down, F4, h0, h1, a.zero_row);
             load_chunk<JF, CHF>(b1, L.w_down, F4, h0 + CHF, h1, a.zero_row);
-            target += a.bar_groups;
-            if (!bar_wait(a, target, flag)) return;
+            target += 1;
+            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- D: down + residual -------------------------------------------------------
             {
@@ -573,27 +651,30 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                                                 e, a.zero_row);
             }
             stamp(a, it, kb, 0);
-            bar_arrive(a.bar, a.bar_groups);
+            bar_arrive(a.flags, target + 1);
             {
+                // chunks 0-1 of the next layer's qkv, or of the lm_head
                 const bool last = l + 1 == a.n_layers;
-                const float* Wn = last ? a.lm_head : a.layers[l + 1].wqkv;
+                const float* Wn = last ? a.lm_head : a.layers[last ? l : l + 1].wqkv;
                 const int n0 = last ? v0 : qa0, n1 = last ? v1 : qa1;
                 load_chunk<1, 8>(b0, Wn, H4, n0, n1, a.zero_row);
                 load_chunk<1, 8>(b1, Wn, H4, n0 + 8, n1, a.zero_row);
             }
-            target += a.bar_groups;
-            if (!bar_wait(a, target, flag)) return;
+            target += 1;
+            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
         }
         // ---- E: lm_head + per-workgroup argmax ---------------------------------------------
         {
+            float4 xr = norm_load(a.x, true, H);
             float4 xv[1];
-            norm_slice(a.x, true, a.final_norm, H, a.eps, scratch, xs, xv);
+            norm_finish(xr, a.final_norm, H, a.eps, scratch, xs, xv);
             Epi e{};
             e.out = a.logits;
             e.best = -FLT_MAX;
             e.best_idx = 0x7fffffff;
-            stream_rows<1, 8, EPI_LOGITS>(a.lm_head, H4, v0, v1, xv, b0, b1, b2, red, rsel, e, a.zero_row);
+            stream_rows<1, 8, EPI_LOGITS>(a.lm_head, H4, v0, v1, xv, b0, b1, b2, red, rsel, e,
+                                          a.zero_row);
             if (t == 0) {
                 const unsigned long long packed =
                     (unsigned long long)__float_as_uint(e.best) |
@@ -603,12 +684,12 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             }
         }
         stamp(a, it, kb, 0);
-        bar_arrive(a.bar, a.bar_groups);
-        // layer 0's first chunks for the next token (after the last token they go unused)
+        bar_arrive(a.flags, target + 1);
+        // qkv chunks of layer 0 for the next token (after the last token they go unused)
         load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
         load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
-        target += a.bar_groups;
-        if (!bar_wait(a, target, flag)) return;
+        target += 1;
+        if (!bar_wait(a, target, okw)) return;
         stamp(a, it, kb++, 1);
         // ---- F: global argmax (lowest index on ties), redundantly in every workgroup ------
         {
@@ -669,7 +750,7 @@ const void* pick_kernel(int jf) {
 
 
 size_t lds_bytes(const PersistArgs& a) {
-    size_t floats = 256 + (size_t)a.hidden + 64 * KSTRIDE + 64 * 64 + 3 * 64;
+    size_t floats = 256 + (size_t)a.hidden + 64 * KSTRIDE + 64 * 64 + 4 * 64 + NW * 64;
     return floats * sizeof(float);
 }
 
@@ -707,6 +788,11 @@ int persist_plan(int device, PersistArgs* ap, int* grid, size_t* lds, std::strin
     int per_cu = 0;
     SHP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, NT, bytes));
     if (per_cu < 1) return no("persistent kernel does not fit on a CU");
+    if (cus > NW * 64) return no("more CUs than barrier-flag pollers");
+    if ((a.hidden + cus - 1) / cus > 8)
+        return no("more than 8 hidden rows per workgroup (hidden > 8 x CUs)");
+    if (((a.n_heads + 2 * a.n_kv) * 64 + cus - 1) / cus > 16)
+        return no("more than 16 qkv rows per workgroup");
     *grid = cus;  // one workgroup per CU
     *lds = bytes;
     return SHP_OK;

@@ -44,9 +44,9 @@ struct Llama {
     int p_grid = 0;
     size_t p_lds = 0;
     std::string p_why;
-    unsigned long long* bar = nullptr;
+    unsigned long long* bar = nullptr;  // barrier flags
     int* abort_flag = nullptr;
-    unsigned long long bar_top = 0;  // top barrier counter value after the last launch
+    unsigned long long bar_top = 0;  // barriers completed by all launches so far
 
     ~Llama() {
         if (exec) (void)hipGraphExecDestroy(exec);
@@ -115,15 +115,15 @@ struct Llama {
         a.prof = prof;
         rc = persist_launch(ctx->stream, a, p_grid, p_lds);
         if (rc) return rc;
-        bar_top += (unsigned long long)n * persist_barriers_per_token(cfg.n_layers) *
-                   (unsigned long long)pa.bar_groups;
+        bar_top += (unsigned long long)n * persist_barriers_per_token(cfg.n_layers);
         // a barrier wait that gave up makes every workgroup exit; report it and re-arm
         int aborted = 0;
         SHP_HIP_CHECK(hipMemcpyAsync(&aborted, abort_flag, sizeof(int), hipMemcpyDeviceToHost,
                                      ctx->stream));
         SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
         if (aborted) {
-            SHP_HIP_CHECK(hipMemsetAsync(bar, 0, kPersistBarSlots * sizeof(unsigned long long),
+            SHP_HIP_CHECK(hipMemsetAsync(bar, 0,
+                                         persist_flag_slots(p_grid) * sizeof(unsigned long long),
                                          ctx->stream));
             SHP_HIP_CHECK(hipMemsetAsync(abort_flag, 0, sizeof(int), ctx->stream));
             SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
@@ -186,9 +186,6 @@ struct Llama {
         int rc = alloc(&zero, zrow);
         if (rc) return rc;
         SHP_HIP_CHECK(hipMemset(zero, 0, zrow * sizeof(float)));
-        SHP_HIP_CHECK(hipMalloc((void**)&bar, kPersistBarSlots * sizeof(unsigned long long)));
-        allocs.push_back(bar);
-        SHP_HIP_CHECK(hipMemset(bar, 0, kPersistBarSlots * sizeof(unsigned long long)));
         SHP_HIP_CHECK(hipMalloc((void**)&abort_flag, sizeof(int)));
         allocs.push_back(abort_flag);
         SHP_HIP_CHECK(hipMemset(abort_flag, 0, sizeof(int)));
@@ -205,7 +202,6 @@ struct Llama {
         pa.logits = logits;
         pa.zero_row = zero;
         pa.st = st;
-        pa.bar = bar;
         pa.abort_flag = abort_flag;
         pa.spin_limit = 1ll << 22;  // ~1 us per poll: a wait gives up after seconds
         pa.n_layers = cfg.n_layers;
@@ -224,7 +220,11 @@ struct Llama {
         SHP_HIP_CHECK(hipMalloc((void**)&cand, (size_t)p_grid * sizeof(ArgmaxCand)));
         allocs.push_back(cand);
         pa.cand = cand;
-        pa.bar_groups = persist_bar_groups(p_grid);
+        const size_t fbytes = persist_flag_slots(p_grid) * sizeof(unsigned long long);
+        SHP_HIP_CHECK(hipMalloc((void**)&bar, fbytes));
+        allocs.push_back(bar);
+        SHP_HIP_CHECK(hipMemset(bar, 0, fbytes));
+        pa.flags = bar;
         return SHP_OK;
     }
 
@@ -399,14 +399,14 @@ int shp_llama_set_engine(shp_llama* p, int engine) {
 
 // Internal profiling hook (not part of include/spirv_hip.h): decodes n tokens with the
 // persistent engine and copies the phase timestamps to host_out, which must hold
-// n * (5 * n_layers + 1) * 4 * grid values; *grid receives the workgroup count.
+// n * (5 * n_layers + 1) * 16 * grid values; *grid receives the workgroup count.
 int shp_llama_profile_persistent(shp_llama* p, int32_t n, unsigned long long* host_out,
                                  uint64_t cap, int32_t* grid) {
     if (!p || !host_out || !grid || n <= 0)
         return fail(SHP_ERR_INVALID, "shp_llama_profile_persistent: bad arguments");
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (lm->p_grid <= 0) return fail(SHP_ERR_UNSUPPORTED, "persistent engine unavailable");
-    const uint64_t need = (uint64_t)n * shp::persist_barriers_per_token(lm->cfg.n_layers) * 4 *
+    const uint64_t need = (uint64_t)n * shp::persist_barriers_per_token(lm->cfg.n_layers) * 16 *
                           (uint64_t)lm->p_grid;
     if (cap < need) return fail(SHP_ERR_INVALID, "shp_llama_profile_persistent: buffer too small");
     unsigned long long* d = nullptr;
