@@ -117,6 +117,29 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int):
     return res
 
 
+def bench_config(ctx, arch: str, batch: int, seq_len: int, steps: int):
+    """Latency of one graph-replayed forward of another benchmark config, with its dense
+    FLOPs (2 x MAC of the convolutions and dots) against the fp32 MFMA peak."""
+    from spirv_inference_amd.models import Model
+    m = Model(ctx, arch, batch, seq_len, seed=2)
+    flops, wbytes = m.work()
+    m.use_graph(True)
+    for _ in range(3):
+        m.run()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.run()
+    ctx.sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    m.close()
+    tflops = flops / (ms / 1e3) / 1e12
+    return {"batch": batch, "seq_len": seq_len or None, "ms_per_forward": round(ms, 4),
+            "gflop_per_forward": round(flops / 1e9, 3), "weight_mb": round(wbytes / 1e6, 2),
+            "achieved_tflops": round(tflops, 3),
+            "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4)}
+
+
 def time_decode(ctx, lm, prompt, n_new: int):
     lm.reset()
     for t in prompt:
@@ -214,6 +237,8 @@ def main() -> int:
                     help="decode steps for the CPU baseline (after the prompt)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the MobileNetV2 / EfficientNet-Lite0 / BERT latency lines")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one `reshape` copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -228,6 +253,14 @@ def main() -> int:
     rn = bench_resnet(ctx, args.steps, args.warmup, args.batch)
     log(f"resnet50 b{args.batch}: {rn['img_s']:.1f} img/s, {rn['ms_per_step']:.3f} ms/step "
         f"(eager+events {rn['eager_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
+    configs = {}
+    if not args.no_configs:
+        for arch, b, sl in (("mobilenet_v2", 1, 0), ("efficientnet_lite0", 8, 0),
+                            ("bert_base", 8, 128)):
+            configs[arch] = bench_config(ctx, arch, b, sl, max(args.steps, 10))
+            c = configs[arch]
+            log(f"{arch} b{b}: {c['ms_per_forward']:.3f} ms/forward, "
+                f"{c['achieved_tflops']:.1f} TFLOP/s ({100 * c['frac_fp32_mfma']:.1f}% of fp32 MFMA)")
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx, args.decode_tokens, args.prompt_tokens)
@@ -299,6 +332,7 @@ def main() -> int:
             "kernel_ms_per_step": round(rn["kernel_ms_per_step"], 4),
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},
             "top1": rn["top1"],
+            "configs": configs,
         },
     }
     if dec is not None:
