@@ -70,6 +70,107 @@ __device__ __forceinline__ void conv_k(const GemmParams& p, int k, int amode, in
     }
 }
 
+// ---- epilogue shared by the GEMM kernels.  Accumulator register r of a 32x32 block holds
+// row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.  The tile goes through LDS (Cs, the
+// kernel's tile buffer, free again when this is called), RC rows at a time, so global stores
+// (and residual loads) are 16-byte and row-contiguous.  With split-K the raw sums go to the
+// partial buffer instead and the reduction pass applies the epilogue.
+template <int BM, int BN, int WM, int WN, int RC, int CS, int CM>
+__device__ __attribute__((always_inline)) inline void gemm_epilogue(
+    const GemmParams& p, const floatx16 (&acc)[BM / WM / 32][BN / WN / 32], float* Cs, int m0,
+    int n0, int split, int bz, int bo, int bi) {
+    constexpr int FM = BM / WM / 32;
+    constexpr int FN = BN / WN / 32;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int lh = lane >> 5;
+    const int bcol = wn * (BN / WN) + (lane & 31);
+    const int nbatch = gridDim.z;
+    const int hw = p.coh * p.cow;
+    float* __restrict__ C = p.c + bo * p.sc_outer + bi * p.sc_inner;
+    const float* __restrict__ R =
+        p.residual ? p.residual + bo * p.sc_outer + bi * p.sc_inner : nullptr;
+    float* __restrict__ P =
+        p.splits > 1 ? p.partial + ((int64_t)split * nbatch + bz) * p.M * p.N : nullptr;
+    const bool vec = P ? (p.N & 3) == 0
+                       : (CM == shp::C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 &&
+                          (p.N & 3) == 0 && (((uintptr_t)C) & 15) == 0 &&
+                          (!p.bias || (((uintptr_t)p.bias) & 15) == 0) &&
+                          (!R || (((uintptr_t)R) & 15) == 0));
+    constexpr int TPR = BN / 4, RPP = 256 / TPR;
+    const int cl4 = (tid % TPR) * 4;
+    const int col4 = n0 + cl4;
+    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (vec && !P && p.bias && col4 < p.N) bv = *reinterpret_cast<const float4*>(p.bias + col4);
+#pragma unroll
+    for (int c0 = 0; c0 < BM; c0 += RC) {
+        if (c0 > 0) __syncthreads();  // the previous chunk has been consumed
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            const int rb = wm * (BM / WM) + fm * 32;
+            if (rb < c0 || rb >= c0 + RC) continue;
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    Cs[(rb - c0 + 8 * (r >> 2) + 4 * lh + (r & 3)) * CS + bcol + fn * 32] =
+                        acc[fm][fn][r];
+        }
+        __syncthreads();
+        if (vec) {
+#pragma unroll 4
+            for (int i = 0; i < RC / RPP; ++i) {
+                const int rl = tid / TPR + RPP * i;
+                const int row = m0 + c0 + rl;
+                if (row >= p.M || col4 >= p.N) continue;
+                float4 v = *reinterpret_cast<const float4*>(&Cs[rl * CS + cl4]);
+                if (P) {
+                    *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
+                    continue;
+                }
+                const int64_t ci = (int64_t)row * p.scm + col4;
+                float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (R) rv = *reinterpret_cast<const float4*>(R + ci);
+                v.x = shpd::apply_act(v.x + bv.x + rv.x, p.act, p.alpha);
+                v.y = shpd::apply_act(v.y + bv.y + rv.y, p.act, p.alpha);
+                v.z = shpd::apply_act(v.z + bv.z + rv.z, p.act, p.alpha);
+                v.w = shpd::apply_act(v.w + bv.w + rv.w, p.act, p.alpha);
+                *reinterpret_cast<float4*>(C + ci) = v;
+            }
+        } else {
+            // scalar path: consecutive threads walk the contiguous direction of C
+            for (int e = tid; e < RC * BN; e += 256) {
+                int rl, cl;
+                if constexpr (CM == shp::C_NCHW) {
+                    rl = e % RC;
+                    cl = e / RC;
+                } else {
+                    rl = e / BN;
+                    cl = e % BN;
+                }
+                const int row = m0 + c0 + rl, col = n0 + cl;
+                if (row >= p.M || col >= p.N) continue;
+                float v = Cs[rl * CS + cl];
+                if (P) {
+                    P[(int64_t)row * p.N + col] = v;
+                    continue;
+                }
+                int64_t ci;
+                if constexpr (CM == shp::C_NCHW) {
+                    const int img = row / hw, pix = row % hw;
+                    ci = ((int64_t)img * p.N + col) * hw + pix;
+                } else {
+                    ci = (int64_t)row * p.scm + (int64_t)col * p.scn;
+                }
+                if (p.bias) v += p.bias[col];
+                if (R) v += R[ci];
+                C[ci] = shpd::apply_act(v, p.act, p.alpha);
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int BK, int AM, int BMD, int CM>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     constexpr int FM = BM / WM / 32;
@@ -361,95 +462,269 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
         }
     }
 
-    // ---- epilogue.  Accumulator register r of a 32x32 block holds row
-    // 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.  The tile goes through LDS, RC rows
-    // at a time, so global stores (and residual loads) are 16-byte and row-contiguous.
-    float* Cs = smem;
-    const int nbatch = gridDim.z;
-    const int hw = p.coh * p.cow;
-    float* __restrict__ C = p.c + bo * p.sc_outer + bi * p.sc_inner;
-    const float* __restrict__ R =
-        p.residual ? p.residual + bo * p.sc_outer + bi * p.sc_inner : nullptr;
-    float* __restrict__ P =
-        p.splits > 1 ? p.partial + ((int64_t)split * nbatch + bz) * p.M * p.N : nullptr;
-    const bool vec = P ? (p.N & 3) == 0
-                       : (CM == shp::C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 &&
-                          (p.N & 3) == 0 && (((uintptr_t)C) & 15) == 0 &&
-                          (!p.bias || (((uintptr_t)p.bias) & 15) == 0) &&
-                          (!R || (((uintptr_t)R) & 15) == 0));
-    constexpr int TPR = BN / 4, RPP = 256 / TPR;
-    const int cl4 = (tid % TPR) * 4;
-    const int col4 = n0 + cl4;
-    float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (vec && !P && p.bias && col4 < p.N) bv = *reinterpret_cast<const float4*>(p.bias + col4);
-#pragma unroll
-    for (int c0 = 0; c0 < BM; c0 += RC) {
-        if (c0 > 0) __syncthreads();  // the previous chunk has been consumed
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            const int rb = wm * (BM / WM) + fm * 32;
-            if (rb < c0 || rb >= c0 + RC) continue;
-#pragma unroll
-            for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    Cs[(rb - c0 + 8 * (r >> 2) + 4 * lh + (r & 3)) * CS + bcol + fn * 32] =
-                        acc[fm][fn][r];
-        }
-        __syncthreads();
-        if (vec) {
-#pragma unroll 4
-            for (int i = 0; i < RC / RPP; ++i) {
-                const int rl = tid / TPR + RPP * i;
-                const int row = m0 + c0 + rl;
-                if (row >= p.M || col4 >= p.N) continue;
-                float4 v = *reinterpret_cast<const float4*>(&Cs[rl * CS + cl4]);
-                if (P) {
-                    *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
-                    continue;
-                }
-                const int64_t ci = (int64_t)row * p.scm + col4;
-                float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (R) rv = *reinterpret_cast<const float4*>(R + ci);
-                v.x = shpd::apply_act(v.x + bv.x + rv.x, p.act, p.alpha);
-                v.y = shpd::apply_act(v.y + bv.y + rv.y, p.act, p.alpha);
-                v.z = shpd::apply_act(v.z + bv.z + rv.z, p.act, p.alpha);
-                v.w = shpd::apply_act(v.w + bv.w + rv.w, p.act, p.alpha);
-                *reinterpret_cast<float4*>(C + ci) = v;
-            }
-        } else {
-            // scalar path: consecutive threads walk the contiguous direction of C
-            for (int e = tid; e < RC * BN; e += 256) {
-                int rl, cl;
-                if constexpr (CM == shp::C_NCHW) {
-                    rl = e % RC;
-                    cl = e / RC;
-                } else {
-                    rl = e / BN;
-                    cl = e % BN;
-                }
-                const int row = m0 + c0 + rl, col = n0 + cl;
-                if (row >= p.M || col >= p.N) continue;
-                float v = Cs[rl * CS + cl];
-                if (P) {
-                    P[(int64_t)row * p.N + col] = v;
-                    continue;
-                }
-                int64_t ci;
-                if constexpr (CM == shp::C_NCHW) {
-                    const int img = row / hw, pix = row % hw;
-                    ci = ((int64_t)img * p.N + col) * hw + pix;
-                } else {
-                    ci = (int64_t)row * p.scm + (int64_t)col * p.scn;
-                }
-                if (p.bias) v += p.bias[col];
-                if (R) v += R[ci];
-                C[ci] = shpd::apply_act(v, p.act, p.alpha);
-            }
-        }
-    }
+    gemm_epilogue<BM, BN, WM, WN, RC, CS, CM>(p, acc, smem, m0, n0, split, bz, bo, bi);
 }
 
+// ---- pipelined variant: operand tiles go from global memory straight into LDS
+// (gfx950 global_load_lds_dwordx4: each lane moves 16 bytes, lane i of a wavefront writes
+// bytes 16i..16i+15 of the 1 KiB block that M0 points at), through a ring of DMA_STAGES
+// K tiles, so nothing is staged in registers and DMA_STAGES-1 tiles are in flight while one
+// is multiplied.  Serves the two row-contiguous operand forms of the model paths: A =
+// row-major rows (A_KVEC) or an NHWC im2col whose K tile sits inside one (ky, kx) tap, and
+// B = [K][N] rows (B_NVEC).
+//
+// LDS layout of one stage (byte offsets):
+//   A  128 rows x 16 k: block b of 16 rows at b*1024, chunk j (k 4j..4j+3) of row r at
+//      (r/16)*1024 + j*256 + (r%16)*16.  A DMA instruction fills one block, lane i taking
+//      row 16b + i%16, chunk i/16; a fragment read (16 lanes, consecutive rows, one chunk)
+//      covers 256 contiguous bytes, so it is free of bank conflicts.
+//   B  16 k rows x BN: each DMA instruction fills 256/BN whole rows (1 KiB) and the blocks
+//      are BPAD bytes apart, so lanes 32-63 (k + 8) land 32 banks away from lanes 0-31.
+// Chunks outside the operand (padding taps, the K tail, rows/columns past M/N) are read
+// from a zero page, so their LDS slots hold zeros.
+__device__ __attribute__((aligned(64))) float g_dma_zero[16];
+
+__device__ __forceinline__ void dma16(const float* src, unsigned lds_byte) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_byte) : "memory");
+}
+
+// Wait until at most N of this wavefront's vector-memory operations are outstanding and
+// its LDS reads are done, then synchronise the workgroup.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+constexpr int DMA_STAGES = 4;
+
+template <int BN>
+struct DmaTile {
+    static constexpr int BM = 128, BK = 16, WM = 2, WN = 2;
+    static constexpr int A_BYTES = BM * BK * 4;              // 8 KiB
+    static constexpr int B_RPI = 256 / BN;                   // B rows per DMA instruction
+    static constexpr int B_INS = BK / B_RPI;                 // DMA instructions per B tile
+    static constexpr int BPAD = BN == 128 ? 32 : 64;
+    static constexpr int B_STRIDE = 1024 + BPAD;
+    static constexpr int STAGE = A_BYTES + B_INS * B_STRIDE;
+    static constexpr int A_PW = BM / 16 / 4;                 // A instructions per wavefront
+    static constexpr int B_PW = B_INS / 4;                   // B instructions per wavefront
+    static constexpr int NDMA = A_PW + B_PW;
+    static constexpr int CS = BN + 4;
+    static constexpr int SMEM = DMA_STAGES * STAGE;
+    static constexpr int RC = BM * CS * 4 <= SMEM ? BM : (BM / 2) * CS * 4 <= SMEM ? BM / 2 : 32;
+    static_assert(B_PW >= 1 && B_INS % 4 == 0, "B tile must split over four wavefronts");
+};
+
+template <int BN, int AM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, BN == 128 ? 2 : 3))) void gemm_dma_kernel(GemmParams p) {
+    using T = DmaTile<BN>;
+    constexpr int BM = T::BM, BK = T::BK, WM = T::WM, WN = T::WN;
+    constexpr int FM = BM / WM / 32;
+    constexpr int FN = BN / WN / 32;
+    static_assert(AM == shp::A_KVEC || AM == shp::A_CONV_NHWC4, "row-contiguous A only");
+    __shared__ __attribute__((aligned(1024))) char smem[T::SMEM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int li = lane & 31, lh = lane >> 5;
+
+    // tile coordinates, each XCD (block id mod 8) taking a contiguous run of tiles
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int ntiles = tiles_m * tiles_n;
+    int bid = blockIdx.x;
+    const int full = (ntiles / 8) * 8;
+    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+    const int m0 = (bid / tiles_n) * BM, n0 = (bid % tiles_n) * BN;
+
+    const int split = blockIdx.y;
+    const int bz = blockIdx.z;
+    const int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
+    const float* __restrict__ A = p.a + bo * p.sa_outer + bi * p.sa_inner;
+    const float* __restrict__ B = p.b + bo * p.sb_outer + bi * p.sb_inner;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int ntk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const float* const zero = g_dma_zero;
+
+    // ---- DMA source coordinates of this lane
+    const int achunk = (lane >> 4) * 4;  // k offset of this lane's A chunk in a K tile
+    ConvRow crow[T::A_PW];
+    const float* arow[T::A_PW];  // row-major A: this lane's chunk at k = 0 (row 0 past M)
+    bool aok[T::A_PW];
+#pragma unroll
+    for (int u = 0; u < T::A_PW; ++u) {
+        const int m = m0 + (wave * T::A_PW + u) * 16 + (lane & 15);
+        aok[u] = m < p.M;
+        if constexpr (AM == shp::A_CONV_NHWC4) crow[u] = conv_row(p, m, AM);
+        else arow[u] = A + (int64_t)(aok[u] ? m : 0) * p.sam + achunk;
+    }
+    const int bn = n0 + (lane % (BN / 4)) * 4;
+    const bool bn_ok = bn < p.N;
+    int bkl[T::B_PW];
+    const float* brow[T::B_PW];  // B: this lane's chunk of row bkl at k tile 0
+#pragma unroll
+    for (int u = 0; u < T::B_PW; ++u) {
+        bkl[u] = (wave * T::B_PW + u) * T::B_RPI + lane / (BN / 4);
+        brow[u] = B + (int64_t)bkl[u] * p.sbk + (bn_ok ? bn : 0);
+    }
+
+    // Position of the next K tile to issue (uniform): its first k and, for a convolution,
+    // its tap (ky, kx) and first channel, advanced tile by tile instead of divided out.
+    int q_tile = 0, q_kt0 = kbeg, q_ic0 = 0, q_kx = 0, q_ky = 0;
+    if constexpr (AM == shp::A_CONV_NHWC4) {
+        q_ic0 = kbeg % p.cic;
+        const int t = kbeg / p.cic;
+        q_kx = t % p.ckw;
+        q_ky = t / p.ckw;
+    }
+    const unsigned lds0 = (unsigned)(uintptr_t)smem;
+
+    // One DMA instruction of the tile at q_*: A block u, B block u.  Every tile issues
+    // exactly NDMA of them per wavefront, a tile past the end reading only the zero page,
+    // so the vmcnt counts below hold on every iteration.
+    // (Conditions use '&' and both addresses exist before the select, so this stays
+    // straight-line code: no exec-masked branches between the MFMAs.)
+    auto dma_a = [&](int u, unsigned sb) __attribute__((always_inline)) {
+        const bool kin = (q_tile < ntk) & (q_kt0 + achunk < kend);
+        const unsigned dst = __builtin_amdgcn_readfirstlane(sb + (wave * T::A_PW + u) * 1024);
+        if constexpr (AM == shp::A_CONV_NHWC4) {
+            const int64_t toff = ((int64_t)q_ky * p.ciw + q_kx) * p.cic + q_ic0 + achunk;
+            const int iy = crow[u].iy0 + q_ky, ix = crow[u].ix0 + q_kx;
+            const bool ok = kin & crow[u].valid & ((unsigned)iy < (unsigned)p.cih) &
+                            ((unsigned)ix < (unsigned)p.ciw);
+            const float* src = A + crow[u].base + toff;
+            dma16(ok ? src : zero, dst);
+        } else {
+            const float* src = arow[u] + q_kt0;
+            dma16(kin & aok[u] ? src : zero, dst);
+        }
+    };
+    auto dma_b = [&](int u, unsigned sb) __attribute__((always_inline)) {
+        const bool ok = (q_tile < ntk) & bn_ok & (q_kt0 + bkl[u] < kend);
+        const float* src = brow[u] + (int64_t)q_kt0 * p.sbk;
+        dma16(ok ? src : zero,
+              __builtin_amdgcn_readfirstlane(sb + T::A_BYTES + (wave * T::B_PW + u) * T::B_STRIDE));
+    };
+    auto advance = [&]() __attribute__((always_inline)) {
+        ++q_tile;
+        q_kt0 += BK;
+        if constexpr (AM == shp::A_CONV_NHWC4) {
+            q_ic0 += BK;
+            if (q_ic0 >= p.cic) {
+                q_ic0 = 0;
+                if (++q_kx == p.ckw) {
+                    q_kx = 0;
+                    ++q_ky;
+                }
+            }
+        }
+    };
+
+    // ---- fragments.  Lanes 0-31 feed k = s and lanes 32-63 k = 8 + s of MFMA step s, so a
+    // lane's A values are chunks 2*lh and 2*lh + 1 of its row; B values are scalars.
+    int aoff[FM][2];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+        const int r = wm * (BM / WM) + fm * 32 + li;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) aoff[fm][c] = ((r >> 4) * 4 + 2 * lh + c) * 256 + (r & 15) * 16;
+    }
+    const int bcol = wn * (BN / WN) + li;
+    constexpr int NRA = 2 * FM;  // A fragment reads (float4) per tile
+    constexpr int NRB = 4 * FN;  // B fragment reads (pairs of k rows) per tile
+    auto read_frag = [&](int j, const char* st, float4 (&af)[FM][2], float (&bf)[FN][8])
+        __attribute__((always_inline)) {
+        if (j < NRA) {
+            af[j / 2][j % 2] = *reinterpret_cast<const float4*>(st + aoff[j / 2][j % 2]);
+        } else {
+            const int fn = (j - NRA) / 4, pr = (j - NRA) % 4;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int k = lh * 8 + 2 * pr + e;
+                bf[fn][2 * pr + e] = *reinterpret_cast<const float*>(
+                    st + T::A_BYTES + (k / T::B_RPI) * T::B_STRIDE + (k % T::B_RPI) * BN * 4 +
+                    (bcol + fn * 32) * 4);
+            }
+        }
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // One K tile: its MFMAs, with the other work of the pipeline slotted between them so the
+    // matrix pipe keeps running: the barrier that publishes tile kt + 1 a quarter of the way
+    // in, then the fragment reads of tile kt + 1 into the other register set, one per MFMA,
+    // and the DMA instructions of tile kt + DMA_STAGES - 1 spread out, half before the
+    // barrier and half after the reads, so the four wavefronts never queue all of theirs
+    // on the CU's address unit at once.
+    constexpr int NM = 8 * FM * FN;
+    constexpr int BAR = NM / 4;
+    constexpr int RD_END = BAR + NRA + NRB;  // last MFMA slot followed by a fragment read
+    constexpr int D_PRE = (T::NDMA + 1) / 2;  // DMA instructions before the barrier
+    constexpr int D_POST = T::NDMA - D_PRE;
+    static_assert(D_PRE <= BAR && RD_END + D_POST < NM, "pipeline slots must fit the MFMAs");
+    auto dma_slot = [](int j) constexpr {
+        return j < D_PRE ? j * (BAR / D_PRE)
+                         : RD_END + 1 + (j - D_PRE) * ((NM - 1 - RD_END) / (D_POST > 0 ? D_POST : 1));
+    };
+    auto tile = [&](int kt, const float4 (&ac)[FM][2], const float (&bc)[FN][8],
+                    float4 (&an)[FM][2], float (&bnx)[FN][8]) __attribute__((always_inline)) {
+        const unsigned sb = lds0 + ((kt + DMA_STAGES - 1) % DMA_STAGES) * T::STAGE;
+        const char* stn = smem + ((kt + 1) % DMA_STAGES) * T::STAGE;
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const int st = i / (FM * FN), fm = (i / FN) % FM, fn = i % FN;
+            const float4& a4 = ac[fm][st >> 2];
+            const int q = st & 3;
+            const float av = q == 0 ? a4.x : q == 1 ? a4.y : q == 2 ? a4.z : a4.w;
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bc[fn][st], acc[fm][fn], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < T::NDMA; ++j) {
+                if (i != dma_slot(j)) continue;
+                if (j < T::A_PW) dma_a(j, sb);
+                else dma_b(j - T::A_PW, sb);
+                if (j == T::NDMA - 1) advance();
+            }
+            // tile kt + 1 has landed for every wavefront (younger: tile kt + 2 and the first
+            // D_PRE instructions of tile kt + 3); every read of tile kt - 1 is done
+            if (i == BAR) dma_wait_barrier<(DMA_STAGES - 3) * T::NDMA + D_PRE>();
+            if (i > BAR && i <= BAR + NRA + NRB) read_frag(i - BAR - 1, stn, an, bnx);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    float4 fa0[FM][2], fa1[FM][2];
+    float fb0[FN][8], fb1[FN][8];
+#pragma unroll
+    for (int s = 0; s < DMA_STAGES - 1; ++s) {
+        const unsigned sb = lds0 + s * T::STAGE;
+#pragma unroll
+        for (int u = 0; u < T::A_PW; ++u) dma_a(u, sb);
+#pragma unroll
+        for (int u = 0; u < T::B_PW; ++u) dma_b(u, sb);
+        advance();
+    }
+    dma_wait_barrier<(DMA_STAGES - 2) * T::NDMA>();
+#pragma unroll
+    for (int j = 0; j < NRA + NRB; ++j) read_frag(j, smem, fa0, fb0);
+    for (int kt = 0; kt < ntk; kt += 2) {
+        tile(kt, fa0, fb0, fa1, fb1);
+        if (kt + 1 < ntk) tile(kt + 1, fa1, fb1, fa0, fb0);
+    }
+    // the ring is reused by the epilogue: drain the trailing (zero-page) DMAs first
+    dma_wait_barrier<0>();
+    gemm_epilogue<BM, BN, WM, WN, T::RC, T::CS, shp::C_STRIDED>(
+        p, acc, reinterpret_cast<float*>(smem), m0, n0, split, bz, bo, bi);
+}
 
 // Split-K second pass: sum the partials in split order, then the epilogue.
 template <int CM>
@@ -530,12 +805,54 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
     int bm, bn, bk;
+    bool dma;  // the pipelined gemm_dma_kernel (BM 128, BK 16) instead of gemm_mfma_kernel
 };
 
 // Internal tuning overrides (0 = automatic); set through shp_tune() by experiments only.
 int g_force_tile = 0;    // 1: 128x128, 2: 128x64, 3: 64x64
 int g_force_bk = 0;      // 16 or 32
 int g_force_splits = 0;  // split-K count
+int g_force_dma = 0;     // pipelined DMA kernel: 0 automatic, -1 never, 1: 128x128, 2: 128x64
+
+// The pipelined kernel takes row-contiguous operands whose 16-byte chunks are aligned:
+// A rows (or an NHWC input whose channel count is a multiple of its K tile) and [K][N] B.
+bool dma_eligible(const GemmParams& p, int am, int bm, int cm) {
+    using namespace shp;
+    if (cm != C_STRIDED || bm != B_NVEC) return false;
+    if (am == A_CONV_NHWC4) {
+        if (p.cic % 16 != 0) return false;
+    } else if (am == A_KVEC) {
+        if (p.sak != 1 || p.K % 4 || p.sam % 4 || p.sa_outer % 4 || p.sa_inner % 4) return false;
+    } else {
+        return false;
+    }
+    return p.N % 4 == 0 && p.sbk % 4 == 0 && p.sb_outer % 4 == 0 && p.sb_inner % 4 == 0 &&
+           ((uintptr_t)p.a & 15) == 0 && ((uintptr_t)p.b & 15) == 0;
+}
+
+// Where the pipelined kernel measured faster than the double-buffered one on MI355X
+// (per-layer sweeps of the ResNet-50 b32 convolutions; on the BERT-base row-major products
+// it measured slower, so those keep the double-buffered kernel): a 128x64 tile without split-K,
+// K from 512 to 1152, and a grid of 192..512 tiles (about one or two per CU).  Shorter
+// K loops spend too much of a 128-row tile in its prologue and epilogue; larger grids
+// run as well on the 64x64 kernel at four workgroups per CU; smaller grids or longer K
+// need split-K, where the 64x64 kernel's finer partials fill the CUs better.
+bool dma_preferred(const GemmParams& p, int nbatch) {
+    const int64_t tiles = (int64_t)((p.M + 127) / 128) * ((p.N + 63) / 64) * nbatch;
+    return p.K >= 512 && p.K <= 1152 && tiles >= 192 && tiles <= 512;
+}
+
+int launch_dma(hipStream_t s, const GemmParams& p, int am, int bn, dim3 grid) {
+    using namespace shp;
+    if (am == A_CONV_NHWC4) {
+        if (bn == 128) hipLaunchKernelGGL((gemm_dma_kernel<128, A_CONV_NHWC4>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_dma_kernel<64, A_CONV_NHWC4>), grid, dim3(256), 0, s, p);
+    } else {
+        if (bn == 128) hipLaunchKernelGGL((gemm_dma_kernel<128, A_KVEC>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_dma_kernel<64, A_KVEC>), grid, dim3(256), 0, s, p);
+    }
+    return SHP_OK;
+}
 
 template <int BM, int BN, int BK, int AM, int BMD, int CM>
 void launch_tile(hipStream_t s, const GemmParams& p, dim3 grid) {
@@ -598,6 +915,7 @@ struct Plan {
 // Workgroups resident per CU, as the compiler reports them for each variant (LDS of the
 // double-buffered tiles out of 160 KiB per CU, and the VGPR+AGPR budget).
 int occupancy(TileCfg t) {
+    if (t.dma) return t.bn == 128 ? 2 : 3;
     if (t.bm == 128 && t.bn == 128) return t.bk == 16 ? 4 : 2;
     if (t.bm == 128) return t.bk == 16 ? 4 : 3;
     return t.bk == 16 ? 8 : 4;
@@ -606,6 +924,7 @@ int occupancy(TileCfg t) {
 // Relative MFMA efficiency of a tile shape and K tile (fitted to per-layer sweeps of the
 // ResNet-50 convolutions on MI355X).
 double tile_eff(TileCfg t) {
+    if (t.dma) return 1.1;
     double e = (t.bm == 128 && t.bn == 128) ? 1.0 : 0.85;
     return t.bk == 16 ? e * 0.85 : e;
 }
@@ -627,17 +946,23 @@ double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps
     return cost;
 }
 
-Plan plan_gemm(const GemmParams& p, int nbatch, bool hot) {
-    static const int kTiles[3][2] = {{128, 128}, {128, 64}, {64, 64}};
+Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv_a) {
+    static const int kTiles[5][2] = {{128, 128}, {128, 64}, {64, 64}, {128, 128}, {128, 64}};
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
-    Plan best{{128, 128, 32}, 1, 0};
+    if (dma_ok && conv_a && g_force_dma == 0 && !g_force_splits && dma_preferred(p, nbatch))
+        return Plan{{128, 64, 16, true}, 1, ((p.K + 31) / 32) * 32};
+    Plan best{{128, 128, 32, false}, 1, 0};
     double best_cost = 1e30;
-    for (int ti = 0; ti < 3; ++ti) {
-        if (g_force_tile && g_force_tile != ti + 1) continue;
+    for (int ti = 0; ti < 5; ++ti) {
+        const bool dma = ti >= 3;
+        if (dma && (!dma_ok || g_force_dma <= 0 || g_force_dma != ti - 2)) continue;
+        if (!dma && dma_ok && g_force_dma > 0) continue;
+        if (!dma && g_force_tile && g_force_tile != ti + 1) continue;
         for (int bk : {32, 16}) {
-            if (bk == 16 && !hot) continue;
-            if (g_force_bk && g_force_bk != bk) continue;
-            TileCfg t{kTiles[ti][0], kTiles[ti][1], bk};
+            if (dma && bk == 32) continue;
+            if (!dma && bk == 16 && !hot) continue;
+            if (!dma && g_force_bk && g_force_bk != bk) continue;
+            TileCfg t{kTiles[ti][0], kTiles[ti][1], bk, dma};
             for (int s : kSplits) {
                 if (g_force_splits && g_force_splits != s) continue;
                 int kps = (p.K + s - 1) / s;
@@ -664,7 +989,8 @@ namespace shp {
 
 size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode) {
     int nbatch = p.batch_outer * p.batch_inner;
-    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode));
+    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
+                        dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4);
     if (pl.splits <= 1) return 0;
     return (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
 }
@@ -709,7 +1035,8 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     int nbatch = p.batch_outer * p.batch_inner;
     if (nbatch <= 0 || nbatch > 65535) return fail(SHP_ERR_SHAPE, "gemm: batch out of range");
     if (amode == A_CONV_NHWC4 && p.cic % 4 != 0) amode = A_CONV_NHWC;
-    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode));
+    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
+                        dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4);
     size_t need = pl.splits > 1 ? (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float) : 0;
     if (pl.splits > 1 && (workspace == nullptr || workspace_bytes < need)) {
         pl.splits = 1;
@@ -723,7 +1050,8 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
     if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
     dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
-    int rc = dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
+    int rc = t.dma ? launch_dma(stream, p, amode, t.bn, grid)
+                 : dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
     if (rc) return rc;
     SHP_HIP_CHECK(hipGetLastError());
     if (p.splits > 1) {
@@ -748,6 +1076,7 @@ extern "C" int shp_tune(const char* key, int value) {
     if (k == "gemm_tile") g_force_tile = value;
     else if (k == "gemm_bk") g_force_bk = value;
     else if (k == "gemm_splits") g_force_splits = value;
+    else if (k == "gemm_dma") g_force_dma = value;
     else return SHP_ERR_INVALID;
     return SHP_OK;
 }

@@ -294,6 +294,81 @@ def test_hlo_conv_full_batch(ctx, orc, ih, ic, k, oc, s):
     assert_close(y, r, 1e-4, 1e-4, "conv b32")
 
 
+# ---- the pipelined GEMM kernel (operand tiles DMA'd straight into LDS) --------------------
+def _tune(key, value):
+    """Internal planner override of the library (shp_tune, not part of the C ABI header)."""
+    from spirv_inference_amd._lib import lib
+    assert lib().shp_tune(key.encode(), int(value)) == 0
+
+
+@pytest.fixture
+def gemm_workspace(ctx):
+    """Split-K partials live in the context workspace, which a model graph sizes."""
+    from spirv_inference_amd.models import Model
+    Model(ctx, "resnet50_v1_5", 32, seed=2).close()
+
+
+# (n, ih, ic, k, oc, stride, split-K): padding taps, M and N tails (oc 20, 132), a strided
+# 1x1, split-K over a long and a short K
+DMA_CONVS = [(2, 5, 16, 3, 20, 1, 0), (1, 9, 32, 3, 132, 2, 0), (3, 14, 48, 1, 72, 2, 0),
+             (2, 7, 512, 3, 64, 1, 2), (1, 7, 64, 3, 64, 1, 3)]
+
+
+@pytest.mark.parametrize("tile", [1, 2], ids=["128x128", "128x64"])
+@pytest.mark.parametrize("n,ih,ic,k,oc,s,splits", DMA_CONVS)
+def test_hlo_conv_dma_pipeline(ctx, orc, gemm_workspace, tile, n, ih, ic, k, oc, s, splits):
+    pad = (k - 1) // 2
+    oh = (ih + 2 * pad - k) // s + 1
+    x = rnd(n, ih, ih, ic)
+    w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+    b, res = rnd(oc, scale=0.01), rnd(n * oh * oh * oc)
+    push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+    try:
+        _tune("gemm_dma", tile)
+        _tune("gemm_splits", splits)
+        y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res,
+                act="relu")
+    finally:
+        _tune("gemm_dma", 0)
+        _tune("gemm_splits", 0)
+    r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res, act="relu")
+    assert_close(y, r, 1e-4, 1e-4, f"dma conv {push[:13]} splits {splits}")
+
+
+@pytest.mark.parametrize("tile", [1, 2], ids=["128x128", "128x64"])
+@pytest.mark.parametrize("bt,m,k,n", [(1, 130, 36, 72), (1, 40, 100, 12), (96, 128, 64, 128)])
+def test_dot_dma_pipeline(ctx, orc, tile, bt, m, k, n):
+    """Row-major A through the pipelined kernel: K tails, M/N tails, strided batches."""
+    a, b = rnd(bt, m, k), rnd(bt, k, n, scale=0.1)
+    bias = rnd(n)
+    try:
+        _tune("gemm_dma", tile)
+        if bt == 1:
+            y = hip(ctx, "hlo_dot_rank2", a[0], b[0], m * n, [m, k, n, m * n], bias=bias,
+                    act="gelu_erf")
+        else:
+            y = hip(ctx, "hlo_dot_batched", a, b, bt * m * n, [bt, m, k, n, bt * m * n])
+    finally:
+        _tune("gemm_dma", 0)
+    if bt == 1:
+        r = orc.run("hlo_dot_rank2", a[0], b[0], m * n, [m, k, n, m * n], bias=bias,
+                    act="gelu_erf")
+    else:
+        r = orc.run("hlo_dot_batched", a, b, bt * m * n, [bt, m, k, n, bt * m * n])
+    assert_close(y, r, 1e-4, 1e-4, f"dma dot {bt}x{m}x{k}x{n}")
+
+
+def test_hlo_conv_dma_by_planner(ctx, orc):
+    """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
+    n, ih, ic, oc = 8, 28, 512, 256
+    x = rnd(n, ih, ih, ic)
+    w = rnd(1, 1, ic, oc, scale=float(np.sqrt(2.0 / ic)))
+    b = rnd(oc, scale=0.01)
+    push = [n, ih, ih, ic, 1, 1, oc, ih, ih, 1, 1, 0, 0, n * ih * ih * oc]
+    y, r = both(ctx, orc, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, act="relu")
+    assert_close(y, r, 1e-4, 1e-4, "conv 6272x256x512")
+
+
 @pytest.mark.parametrize("n,ic,hw,oc,k,s,pad", [(1, 3, 224, 32, 3, 2, 0), (2, 6, 13, 10, 3, 1, 1),
                                                 (1, 32, 28, 64, 1, 1, 0), (2, 5, 9, 7, 5, 2, 2)])
 def test_conv2d_reference_and_nhwc(ctx, orc, n, ic, hw, oc, k, s, pad):
