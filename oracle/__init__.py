@@ -80,14 +80,19 @@ def _f32(a) -> np.ndarray:
 
 
 def run(name: str, in0, in1, n_out: int, push: Sequence[int], bias=None, residual=None,
-        act: str | int = 0, alpha: float = 0.0) -> np.ndarray:
-    """Run one reference kernel on the CPU; returns the output as float32."""
+        act: str | int = 0, alpha: float = 0.0, out_init=None) -> np.ndarray:
+    """Run one reference kernel on the CPU; returns the output as float32.
+
+    `out_init` is the output buffer's content on entry (zeros by default), for the ops that
+    keep part of it: hlo_select (on_false) and hlo_concatenate_into (the other slabs)."""
     # an absent binding is NULL (optional inputs such as softmax_rows' mask test for it)
     a0 = _f32(in0) if in0 is not None else None
     a1 = _f32(in1) if in1 is not None else None
     b = _f32(bias) if bias is not None else None
     r = _f32(residual) if residual is not None else None
     out = np.zeros(max(1, n_out), dtype=np.float32)
+    if out_init is not None:
+        out[:n_out] = _f32(out_init)[:n_out]
     parr = (C.c_int32 * max(1, len(push)))(*[int(p) for p in push])
     act_code = ACT[act] if isinstance(act, str) else int(act)
     rc = lib().orc_run_kernel(name.encode(), a0.ctypes.data if a0 is not None else None,

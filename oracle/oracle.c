@@ -561,6 +561,101 @@ static void rownorm(const float* in, const float* w, float* out, int rows, int c
     }
 }
 
+/* ---- HLO host shape ops (source/xla_hlo/src/compiler.rs), restated the way the Rust
+ * helpers run them: per element, unravel the index (unravel :1299-1307), map the
+ * coordinate, ravel it (ravel :1309-1315). */
+#define HMAX 8
+static int64_t h_elems(const int32_t* d, int r) {
+    int64_t n = 1;
+    for (int k = 0; k < r; ++k) n *= d[k];
+    return n;
+}
+static void h_unravel(int64_t idx, const int32_t* shape, int r, int64_t* c) {
+    int64_t st[HMAX], s = 1;
+    for (int k = r - 1; k >= 0; --k) {
+        st[k] = s;
+        s *= shape[k];
+    }
+    for (int k = 0; k < r; ++k) {
+        c[k] = idx / st[k];
+        idx %= st[k];
+    }
+}
+static int64_t h_ravel(const int64_t* c, const int32_t* shape, int r) {
+    int64_t s = 1, idx = 0;
+    for (int k = r - 1; k >= 0; --k) {
+        idx += c[k] * s;
+        s *= shape[k];
+    }
+    return idx;
+}
+static int h_dims_ok(const int32_t* d, int r) {
+    if (r < 0 || r > HMAX) return 0;
+    for (int k = 0; k < r; ++k)
+        if (d[k] <= 0) return 0;
+    return 1;
+}
+
+/* broadcast_tensor :1361-1393 with explicit `dimensions` (map[a] = output axis of a) */
+static int h_broadcast(const float* src, const int32_t* sd, int rs, const int32_t* map,
+                       float* out, const int32_t* od, int ro) {
+    int64_t n_out = h_elems(od, ro), n_src = h_elems(sd, rs);
+    int same = rs == ro;
+    for (int k = 0; same && k < rs; ++k) same = sd[k] == od[k];
+    if (n_src == n_out && same) {
+        memcpy(out, src, (size_t)n_out * sizeof(float));
+        return 0;
+    }
+    if (n_src == 1) {
+        for (int64_t i = 0; i < n_out; ++i) out[i] = src[0];
+        return 0;
+    }
+    for (int a = 0; a < rs; ++a)
+        if (map[a] < 0 || map[a] >= ro || (sd[a] != 1 && sd[a] != od[map[a]])) return -1;
+    for (int64_t idx = 0; idx < n_out; ++idx) {
+        int64_t oc[HMAX], sc[HMAX];
+        h_unravel(idx, od, ro, oc);
+        for (int a = 0; a < rs; ++a) sc[a] = sd[a] == 1 ? 0 : oc[map[a]];
+        out[idx] = src[h_ravel(sc, sd, rs)];
+    }
+    return 0;
+}
+
+/* binary_tensor :1521-1564 operand rule: as many values as the output -> used flat, else
+ * broadcast_tensor with infer_broadcast_dims :1566-1572 (trailing alignment). */
+static int h_operand(const float* src, const int32_t* sd, int rs, float* out, const int32_t* od,
+                     int ro) {
+    int64_t n_out = h_elems(od, ro);
+    if (h_elems(sd, rs) == n_out) {
+        memcpy(out, src, (size_t)n_out * sizeof(float));
+        return 0;
+    }
+    if (rs > ro) return h_elems(sd, rs) == 1 ? h_broadcast(src, sd, rs, NULL, out, od, ro) : -1;
+    int32_t map[HMAX];
+    for (int a = 0; a < rs; ++a) map[a] = a + (ro - rs);
+    return h_broadcast(src, sd, rs, map, out, od, ro);
+}
+
+/* reduce_tensor :1730-1759: walk the source in index order, fold into the kept coordinate */
+static void h_reduce(const float* src, const int32_t* sd, int r, const int32_t* red, int kind,
+                     float init, float* out, int64_t n_out) {
+    for (int64_t i = 0; i < n_out; ++i) out[i] = init;
+    int32_t od[HMAX];
+    int ro = 0;
+    for (int k = 0; k < r; ++k)
+        if (!red[k]) od[ro++] = sd[k];
+    int64_t n = h_elems(sd, r);
+    for (int64_t idx = 0; idx < n; ++idx) {
+        int64_t c[HMAX], oc[HMAX];
+        h_unravel(idx, sd, r, c);
+        int j = 0;
+        for (int k = 0; k < r; ++k)
+            if (!red[k]) oc[j++] = c[k];
+        int64_t o = ro ? h_ravel(oc, od, ro) : 0;
+        out[o] = kind ? fmaxf(out[o], src[idx]) : out[o] + src[idx];
+    }
+}
+
 static const char* kNames[] = {
     "abs", "exp", "log", "neg", "sqrt", "rsqrt", "sigmoid", "logistic", "tanh", "relu", "relu6",
     "sine", "reshape", "leaky_relu", "add", "sub", "mul", "div", "pow", "min", "max", "concat",
@@ -570,7 +665,9 @@ static const char* kNames[] = {
     "softmax10", "softmax1000", "global_avg_pool_nhwc", "softmax_rows", "layernorm_rows",
     "rmsnorm_rows", "hlo_conv_nhwc_hwio", "conv2d", "fully_connected", "hlo_dot_batched",
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
-    "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows"};
+    "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
+    "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
+    "hlo_reduce"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -834,6 +931,146 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
             int32_t idx = orc_argmax_first(in0 + (int64_t)r * cols, (size_t)cols);
             memcpy(&out[r], &idx, 4);
         }
+        return 0;
+    }
+    if (!strcmp(name, "hlo_broadcast")) { /* compiler.rs:336-347 */
+        NEED(3);
+        int rs = push[0], ro = push[1];
+        if (rs < 0 || rs > HMAX || ro < 1 || ro > HMAX) return orc_fail(-4, "hlo_broadcast: rank");
+        NEED(3 + 2 * rs + ro);
+        const int32_t *sd = push + 3, *od = push + 3 + rs, *map = push + 3 + rs + ro;
+        if (!h_dims_ok(sd, rs) || !h_dims_ok(od, ro) || h_elems(od, ro) != push[2])
+            return orc_fail(-4, "hlo_broadcast: dims");
+        TOTAL(push[2]);
+        if (h_broadcast(in0, sd, rs, map, out, od, ro)) return orc_fail(-4, "hlo_broadcast: dimensions");
+        return 0;
+    }
+    if (!strcmp(name, "hlo_transpose")) { /* compiler.rs:374-386, transpose_tensor :1395-1418 */
+        NEED(2);
+        int r = push[0];
+        if (r < 1 || r > HMAX) return orc_fail(-4, "hlo_transpose: rank");
+        NEED(2 + 2 * r);
+        const int32_t *sd = push + 2, *perm = push + 2 + r;
+        if (!h_dims_ok(sd, r) || h_elems(sd, r) != push[1]) return orc_fail(-4, "hlo_transpose: dims");
+        TOTAL(push[1]);
+        int32_t od[HMAX];
+        int seen = 0, ident = 1;
+        for (int i = 0; i < r; ++i) {
+            if (perm[i] < 0 || perm[i] >= r || ((seen >> perm[i]) & 1)) return orc_fail(-4, "hlo_transpose: perm");
+            seen |= 1 << perm[i];
+            ident &= perm[i] == i;
+            od[i] = sd[perm[i]];
+        }
+        if (ident) {
+            memcpy(out, in0, n_out * sizeof(float));
+            return 0;
+        }
+        for (int64_t idx = 0; idx < (int64_t)n_out; ++idx) {
+            int64_t oc[HMAX], sc[HMAX];
+            h_unravel(idx, od, r, oc);
+            for (int i = 0; i < r; ++i) sc[perm[i]] = oc[i];
+            out[idx] = in0[h_ravel(sc, sd, r)];
+        }
+        return 0;
+    }
+    if (!strcmp(name, "hlo_slice")) { /* compiler.rs:570-582, cpu_slice :1931-1952 */
+        NEED(2);
+        int r = push[0];
+        if (r < 1 || r > HMAX) return orc_fail(-4, "hlo_slice: rank");
+        NEED(2 + 4 * r);
+        const int32_t *sd = push + 2, *st = push + 2 + r, *lim = push + 2 + 2 * r, *sp = push + 2 + 3 * r;
+        if (!h_dims_ok(sd, r)) return orc_fail(-4, "hlo_slice: dims");
+        int32_t od[HMAX];
+        for (int k = 0; k < r; ++k) {
+            if (st[k] < 0 || sp[k] < 1 || lim[k] <= st[k]) return orc_fail(-4, "hlo_slice: spec");
+            od[k] = (lim[k] - st[k] + sp[k] - 1) / sp[k];
+        }
+        if (h_elems(od, r) != push[1]) return orc_fail(-4, "hlo_slice: total");
+        TOTAL(push[1]);
+        for (int64_t idx = 0; idx < (int64_t)n_out; ++idx) {
+            int64_t oc[HMAX], sc[HMAX];
+            int in = 1;
+            h_unravel(idx, od, r, oc);
+            for (int k = 0; k < r; ++k) {
+                sc[k] = st[k] + oc[k] * sp[k];
+                in &= sc[k] < sd[k];
+            }
+            out[idx] = in ? in0[h_ravel(sc, sd, r)] : 0.0f;
+        }
+        return 0;
+    }
+    if (!strcmp(name, "hlo_concatenate_into")) { /* compiler.rs:554-569, cpu_concatenate :1879-1895 */
+        NEED(3);
+        int r = push[0], dim = push[1], offset = push[2];
+        if (r < 1 || r > HMAX || dim < 0 || dim >= r || offset < 0) return orc_fail(-4, "hlo_concatenate_into: rank/dim");
+        NEED(3 + 2 * r);
+        const int32_t *od = push + 3, *id = push + 3 + r;
+        if (!h_dims_ok(od, r) || !h_dims_ok(id, r)) return orc_fail(-4, "hlo_concatenate_into: dims");
+        TOTAL(h_elems(od, r));
+        int64_t n = h_elems(id, r);
+        for (int64_t idx = 0; idx < n; ++idx) {
+            int64_t c[HMAX];
+            int in = 1;
+            h_unravel(idx, id, r, c);
+            c[dim] += offset;
+            for (int k = 0; k < r; ++k) in &= c[k] < od[k];
+            if (in) out[h_ravel(c, od, r)] = in0[idx];
+        }
+        return 0;
+    }
+    if (!strcmp(name, "hlo_compare") || !strcmp(name, "hlo_select")) {
+        /* compare: compiler.rs:511-537 over binary_tensor; select: select_tensor :1574-1620
+         * with on_false already in `out` */
+        int sel = !strcmp(name, "hlo_select");
+#define Q(k) push[(k) - sel] /* field k of the compare layout; select lacks field 0 */
+        NEED(5 - sel);
+        int ro = Q(2), ra = Q(3), rb = Q(4);
+        if (ro < 1 || ro > HMAX || ra < 0 || ra > HMAX || rb < 0 || rb > HMAX) return orc_fail(-4, "compare/select: rank");
+        NEED(5 - sel + ro + ra + rb);
+        const int32_t *od = push + 5 - sel, *ad = od + ro, *bd = od + ro + ra;
+        if (!h_dims_ok(od, ro) || !h_dims_ok(ad, ra) || !h_dims_ok(bd, rb) || h_elems(od, ro) != Q(1))
+            return orc_fail(-4, "compare/select: dims");
+        TOTAL(Q(1));
+        int dir = sel ? 0 : Q(0);
+#undef Q
+        float* a = (float*)malloc(n_out * sizeof(float));
+        float* b = (float*)malloc(n_out * sizeof(float));
+        int bad = !a || !b || h_operand(in0, ad, ra, a, od, ro) || h_operand(in1, bd, rb, b, od, ro);
+        if (!bad) {
+            for (size_t i = 0; i < n_out; ++i) {
+                if (sel) {
+                    if (a[i] != 0.0f) out[i] = b[i];
+                    continue;
+                }
+                int t;
+                switch (dir) {
+                    case 0: t = a[i] < b[i]; break;
+                    case 1: t = a[i] <= b[i]; break;
+                    case 2: t = a[i] == b[i]; break;
+                    case 3: t = a[i] != b[i]; break;
+                    case 4: t = a[i] >= b[i]; break;
+                    default: t = a[i] > b[i]; break;
+                }
+                out[i] = t ? 1.0f : 0.0f;
+            }
+        }
+        free(a);
+        free(b);
+        return bad ? orc_fail(-4, "compare/select: operand does not broadcast") : 0;
+    }
+    if (!strcmp(name, "hlo_reduce")) { /* compiler.rs:939-1007 rank > 4 path: reduce_tensor */
+        NEED(4);
+        int r = push[1];
+        if (r < 1 || r > HMAX || (push[0] != 0 && push[0] != 1)) return orc_fail(-4, "hlo_reduce: rank/kind");
+        NEED(4 + 2 * r);
+        const int32_t *sd = push + 4, *red = push + 4 + r;
+        if (!h_dims_ok(sd, r)) return orc_fail(-4, "hlo_reduce: dims");
+        int64_t kept = 1;
+        for (int k = 0; k < r; ++k)
+            if (!red[k]) kept *= sd[k];
+        if (kept != push[2]) return orc_fail(-4, "hlo_reduce: total");
+        TOTAL(push[2]);
+        h_reduce(in0, sd, r, red, push[0], bits_to_f32(push[3]), out, (int64_t)n_out);
         return 0;
     }
     char msg[128];

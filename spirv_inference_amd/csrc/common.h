@@ -57,6 +57,8 @@ extern KernelEntry kGemmKernels[];
 extern const int kGemmKernelCount;
 extern KernelEntry kSpatialKernels[];
 extern const int kSpatialKernelCount;
+extern KernelEntry kHloOpKernels[];
+extern const int kHloOpKernelCount;
 extern KernelEntry kDecodeKernels[];
 extern const int kDecodeKernelCount;
 

@@ -42,6 +42,7 @@ std::vector<const KernelEntry*>& registry() {
         add(kGemmKernels, kGemmKernelCount);
         add(kSpatialKernels, kSpatialKernelCount);
         add(kDecodeKernels, kDecodeKernelCount);
+        add(kHloOpKernels, kHloOpKernelCount);
         return r;
     }();
     return reg;

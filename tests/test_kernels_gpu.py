@@ -445,3 +445,124 @@ def test_errors_fail_closed(ctx):
     with pytest.raises(ShpError, match="UNSUPPORTED"):
         ctx.launch("add", t, t, t, [8], act="relu")
     t.free()
+
+
+# ---- the HLO path's host shape ops, on the device (compiler.rs:336-586) --------------------
+def _dev(ctx, name, x, y, n_out, push, init=None):
+    tx = ctx.tensor(np.atleast_1d(x)) if x is not None else None
+    ty = ctx.tensor(np.atleast_1d(y)) if y is not None else None
+    out = ctx.tensor(init) if init is not None else ctx.empty(n_out)
+    print(f"[gpu] {name} push={list(push)[:12]} n_out={n_out}", flush=True)
+    ctx.launch(name, tx, ty, out, push)
+    ctx.sync()
+    r = out.download()
+    for t in (tx, ty, out):
+        if t is not None:
+            t.free()
+    return r
+
+
+@pytest.mark.parametrize("src,out,dims", [((4, 1, 64, 64), (4, 8, 64, 64), (0, 1, 2, 3)),
+                                          ((3, 5), (5, 2, 3), (2, 0)), ((1,), (2, 3, 4), (1,)),
+                                          ((2048,), (8, 128, 2048), (2,)),
+                                          ((1, 4, 1, 64, 64), (1, 4, 8, 64, 64), (0, 1, 2, 3, 4))])
+def test_hlo_broadcast(ctx, orc, src, out, dims):
+    from spirv_inference_amd import hlo_ops as H
+    x, n, push = rnd(*src), int(np.prod(out)), H.broadcast_push(src, out, dims)
+    np.testing.assert_array_equal(_dev(ctx, "hlo_broadcast", x, None, n, push),
+                                  orc.run("hlo_broadcast", x, None, n, push))
+
+
+@pytest.mark.parametrize("shape,perm", [((1, 64, 32, 64), (0, 2, 1, 3)), ((8, 128, 12, 64), (0, 2, 3, 1)),
+                                        ((2, 3, 4, 5, 6), (4, 0, 3, 1, 2))])
+def test_hlo_transpose(ctx, orc, shape, perm):
+    from spirv_inference_amd import hlo_ops as H
+    x, push = rnd(*shape), H.transpose_push(shape, perm)
+    np.testing.assert_array_equal(_dev(ctx, "hlo_transpose", x, None, x.size, push),
+                                  orc.run("hlo_transpose", x, None, x.size, push))
+
+
+@pytest.mark.parametrize("shape,starts,limits,strides", [
+    ((1, 32, 64, 64), (0, 0, 0, 0), (1, 32, 64, 32), (1, 1, 1, 1)),
+    ((1, 32, 64, 64), (0, 0, 0, 32), (1, 32, 64, 64), (1, 1, 1, 1)),
+    ((5, 9, 7), (1, 0, 2), (5, 9, 7), (2, 3, 2)), ((4, 6), (0, 2), (4, 9), (1, 1)),
+    ((4, 6), (0, 7), (4, 9), (1, 1))])
+def test_hlo_slice(ctx, orc, shape, starts, limits, strides):
+    from spirv_inference_amd import hlo_ops as H
+    x, push = rnd(*shape), H.slice_push(shape, starts, limits, strides)
+    n = int(np.prod(H.slice_shape(starts, limits, strides)))
+    np.testing.assert_array_equal(_dev(ctx, "hlo_slice", x, None, n, push),
+                                  orc.run("hlo_slice", x, None, n, push))
+
+
+def test_hlo_concatenate(ctx, orc):
+    """Rotate-half's concatenate (two halves on the last axis) and a three-way axis-1 join."""
+    from spirv_inference_amd import hlo_ops as H
+    for shapes, dim in (([(1, 32, 64, 32), (1, 32, 64, 32)], 3), ([(2, 3, 5), (2, 4, 5), (2, 1, 5)], 1)):
+        xs = [rnd(*s) for s in shapes]
+        out_shape = list(shapes[0])
+        out_shape[dim] = sum(s[dim] for s in shapes)
+        n = int(np.prod(out_shape))
+        ts = [ctx.tensor(x) for x in xs]
+        out = ctx.tensor(np.zeros(n, np.float32))
+        H.concatenate(ctx, list(zip(ts, shapes)), dim, out, out_shape)
+        ctx.sync()
+        y = out.download()
+        for t in ts + [out]:
+            t.free()
+        r, off = np.zeros(n, np.float32), 0
+        for x, s in zip(xs, shapes):
+            r = orc.run("hlo_concatenate_into", x, None, n,
+                        H.concatenate_into_push(out_shape, s, dim, off), out_init=r)
+            off += s[dim]
+        np.testing.assert_array_equal(y, r)
+        np.testing.assert_array_equal(y, np.concatenate(xs, axis=dim).reshape(-1))
+
+
+@pytest.mark.parametrize("direction", ["LT", "LE", "EQ", "NE", "GE", "GT"])
+def test_hlo_compare(ctx, orc, direction):
+    from spirv_inference_amd import hlo_ops as H
+    for out, a, b in (((8, 128, 3072), (8, 128, 3072), (1,)), ((4, 5, 6), (5, 6), (4, 1, 6))):
+        x, z = np.round(rnd(*a) * 2) / 2, np.round(rnd(*b) * 2) / 2
+        n, push = int(np.prod(out)), H.compare_push(direction, out, a, b)
+        np.testing.assert_array_equal(_dev(ctx, "hlo_compare", x, z, n, push),
+                                      orc.run("hlo_compare", x, z, n, push))
+
+
+def test_hlo_select(ctx, orc):
+    """select_tensor on the device: on_false broadcast into the output, then hlo_select."""
+    from spirv_inference_amd import hlo_ops as H
+    for out, p, t, f in (((8, 128, 3072), (8, 128, 3072), (8, 128, 3072), (1,)),
+                         ((4, 5, 6), (5, 6), (1, 6), (4, 5, 6))):
+        pred, on_t, on_f = (rnd(*p) > 0).astype(np.float32), rnd(*t), rnd(*f)
+        n = int(np.prod(out))
+        tp, tt, tf, to = ctx.tensor(pred), ctx.tensor(on_t), ctx.tensor(on_f), ctx.empty(n)
+        H.select(ctx, tp, p, tt, t, tf, f, to, out)
+        ctx.sync()
+        y = to.download()
+        for x in (tp, tt, tf, to):
+            x.free()
+        fill = np.broadcast_to(on_f.reshape(f), out).astype(np.float32).reshape(-1)
+        r = orc.run("hlo_select", pred, on_t, n, H.select_push(out, p, t), out_init=fill)
+        np.testing.assert_array_equal(y, r)
+
+
+@pytest.mark.parametrize("shape,dims", [((1, 4, 8, 64, 64), (4,)), ((1, 4, 8, 64, 64), (0, 2)),
+                                        ((3, 5, 7, 2, 3, 4), (1, 2, 5)), ((32, 7, 7, 2048), (1, 2))])
+def test_hlo_reduce(ctx, orc, shape, dims):
+    """Sum folds in source order on both sides, so it is bit-exact like max."""
+    from spirv_inference_amd import hlo_ops as H
+    x = rnd(*shape)
+    kept = int(np.prod([d for k, d in enumerate(shape) if k not in dims]))
+    for kind, init in (("sum", 0.0), ("max", -np.inf)):
+        push = H.reduce_push(kind, shape, dims, init)
+        np.testing.assert_array_equal(_dev(ctx, "hlo_reduce", x, None, kept, push),
+                                      orc.run("hlo_reduce", x, None, kept, push))
+
+
+def test_hlo_shape_ops_fail_closed(ctx):
+    from spirv_inference_amd import hlo_ops as H
+    with pytest.raises(RuntimeError):  # not a permutation
+        _dev(ctx, "hlo_transpose", rnd(4), None, 4, [2, 4, 2, 2, 0, 0])
+    with pytest.raises(RuntimeError):  # total does not match the output
+        _dev(ctx, "hlo_slice", rnd(4, 6), None, 5, H.slice_push((4, 6), (0, 0), (2, 6)))
