@@ -8,7 +8,9 @@ so the token ids are only meaningful for parity and timing.
 
     python -m spirv_inference_amd.generate --tokens 20 --repeat 3
 
-prints the generated ids and the decode time per token of each repetition.  With
+prints the generated ids and the decode time per token of each repetition.  Real weights
+supplied locally replace the seeded ones: `--reference-fixture DIR` (export_llama.py's
+raw-f32 parameter files) or `--safetensors FILE` (a Hugging Face checkpoint).  With
 `--profile-phases N` it also decodes N tokens in one persistent launch with the in-kernel phase
 stamps on and prints, for the last of them, the time each workgroup spends in the phases of a
 layer and at the grid barriers between them (means over workgroups, summed over layers).
@@ -70,6 +72,10 @@ def main() -> int:
     ap.add_argument("--prompt-seed", type=int, default=3)
     ap.add_argument("--engine", choices=("default", "persistent", "graph", "kernels"),
                     default="default")
+    ap.add_argument("--reference-fixture", metavar="DIR",
+                    help="load export_llama.py raw-f32 parameters from DIR")
+    ap.add_argument("--safetensors", metavar="FILE", nargs="+",
+                    help="load a Hugging Face safetensors checkpoint (one file or shards)")
     ap.add_argument("--profile-phases", type=int, default=0, metavar="N",
                     help="after the timed runs, stamp-profile N tokens of the persistent engine")
     args = ap.parse_args()
@@ -77,6 +83,12 @@ def main() -> int:
     prompt = [int(t) for t in rng.integers(0, TINYLLAMA["vocab"], args.prompt_tokens)]
     with Context("any") as ctx:
         lm = Llama(ctx, seed=args.seed)
+        if args.reference_fixture:
+            from .weights import load_llama_reference_fixture
+            load_llama_reference_fixture(lm, args.reference_fixture)
+        elif args.safetensors:
+            from .weights import load_llama_safetensors
+            load_llama_safetensors(lm, args.safetensors)
         if args.engine != "default":
             lm.set_engine(args.engine)
         print(f"engine {lm.engine}", flush=True)

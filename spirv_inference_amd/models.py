@@ -184,11 +184,16 @@ class Llama:
         check(lib().shp_llama_logits(self.handle, C.byref(p), C.byref(n)), "shp_llama_logits")
         return DeviceTensor(self.ctx, n.value, ptr=p.value, owned=False).download()
 
-    def weight(self, layer: int, which: str) -> np.ndarray:
+    def weight_ptr(self, layer: int, which: str) -> tuple[int, int]:
+        """Device address and element count of a weight tensor (see shp_llama_weight)."""
         p, n = C.c_void_p(), C.c_uint64()
         check(lib().shp_llama_weight(self.handle, layer, which.encode(), C.byref(p), C.byref(n)),
               "shp_llama_weight")
-        return DeviceTensor(self.ctx, n.value, ptr=p.value, owned=False).download()
+        return p.value, n.value
+
+    def weight(self, layer: int, which: str) -> np.ndarray:
+        p, n = self.weight_ptr(layer, which)
+        return DeviceTensor(self.ctx, n, ptr=p, owned=False).download()
 
     def weight_bytes(self) -> float:
         b = C.c_double()

@@ -194,3 +194,73 @@ def test_tinyllama_full_greedy_tokens(ctx, orc):
         lm.set_engine("graph")
         assert lm.generate(prompt, 20) == got
         assert_close(lm.logits(), gpu_last, 1e-4, 1e-4, "graph vs persistent logits")
+
+
+def _export_reference_style(lm, cfg, d, prefix="tinyllama"):
+    """Write lm's weights the way export_llama.py lays them out (params in list order,
+    projections [in, out]), plus the separate embedding table."""
+    H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["n_layers"]
+    qd, kvd, hd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["head_dim"]
+    S = cfg["max_seq"]
+    inv = 1.0 / (cfg["rope_theta"] ** (np.arange(0, hd, 2, dtype=np.float32) / hd))
+    emb = np.concatenate([np.outer(np.arange(S, dtype=np.float32), inv)] * 2, axis=-1)
+    params = [np.zeros((1, S, H), np.float32), np.cos(emb).astype(np.float32),
+              np.sin(emb).astype(np.float32), np.zeros((1, 1, S, S), np.float32)]
+    for l in range(L):
+        wqkv = lm.weight(l, "wqkv").reshape(qd + 2 * kvd, H)
+        gu = lm.weight(l, "w_gate_up").reshape(F, 2, H)
+        params += [lm.weight(l, "attn_norm"), wqkv[:qd].T, wqkv[qd:qd + kvd].T, wqkv[qd + kvd:].T,
+                   lm.weight(l, "wo").reshape(H, qd).T, lm.weight(l, "ffn_norm"), gu[:, 0].T,
+                   gu[:, 1].T, lm.weight(l, "w_down").reshape(H, F).T]
+    params += [lm.weight(-1, "final_norm"), lm.weight(-1, "lm_head").reshape(V, H).T]
+    for i, p in enumerate(params):
+        np.ascontiguousarray(p, "<f4").tofile(d / f"{prefix}_param_{i:03d}_p.raw.f32")
+    lm.weight(-1, "embed").astype("<f4").tofile(d / f"{prefix}_token_embedding.raw.f32")
+
+
+def _export_safetensors(lm, cfg, path):
+    from safetensors.numpy import save_file
+    H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["n_layers"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    t = {"model.embed_tokens.weight": lm.weight(-1, "embed").reshape(V, H),
+         "model.norm.weight": lm.weight(-1, "final_norm"),
+         "lm_head.weight": lm.weight(-1, "lm_head").reshape(V, H)}
+    for l in range(L):
+        p = f"model.layers.{l}."
+        wqkv = lm.weight(l, "wqkv").reshape(qd + 2 * kvd, H)
+        gu = lm.weight(l, "w_gate_up").reshape(F, 2, H)
+        t.update({p + "input_layernorm.weight": lm.weight(l, "attn_norm"),
+                  p + "self_attn.q_proj.weight": wqkv[:qd], p + "self_attn.k_proj.weight": wqkv[qd:qd + kvd],
+                  p + "self_attn.v_proj.weight": wqkv[qd + kvd:],
+                  p + "self_attn.o_proj.weight": lm.weight(l, "wo").reshape(H, qd),
+                  p + "post_attention_layernorm.weight": lm.weight(l, "ffn_norm"),
+                  p + "mlp.gate_proj.weight": gu[:, 0], p + "mlp.up_proj.weight": gu[:, 1],
+                  p + "mlp.down_proj.weight": lm.weight(l, "w_down").reshape(H, F)})
+    save_file({k: np.ascontiguousarray(v) for k, v in t.items()}, str(path))
+
+
+LLAMA_WEIGHTS = ["embed", "final_norm", "lm_head"]
+LLAMA_LAYER_WEIGHTS = ["attn_norm", "wqkv", "wo", "ffn_norm", "w_gate_up", "w_down"]
+
+
+@pytest.mark.parametrize("source", ["reference_raw_f32", "safetensors"])
+def test_llama_weight_loaders(ctx, tmp_path, source):
+    """Weights written in the reference's raw-f32 parameter layout (or HF safetensors) and
+    loaded into a decoder with other seeded weights reproduce the source decoder exactly."""
+    from spirv_inference_amd import weights as W
+    from spirv_inference_amd.models import Llama
+    rng = np.random.default_rng(4)
+    prompt = [int(t) for t in rng.integers(0, SMALL["vocab"], 9)]
+    with Llama(ctx, seed=5, **SMALL) as src, Llama(ctx, seed=9, **SMALL) as dst:
+        if source == "safetensors":
+            _export_safetensors(src, SMALL, tmp_path / "model.safetensors")
+            W.load_llama_safetensors(dst, tmp_path / "model.safetensors")
+        else:
+            _export_reference_style(src, SMALL, tmp_path)
+            W.load_llama_reference_fixture(dst, tmp_path)
+        for w in LLAMA_WEIGHTS:
+            assert src.weight(-1, w).tobytes() == dst.weight(-1, w).tobytes(), w
+        for l in range(SMALL["n_layers"]):
+            for w in LLAMA_LAYER_WEIGHTS:
+                assert src.weight(l, w).tobytes() == dst.weight(l, w).tobytes(), (l, w)
+        assert dst.generate(prompt, 6) == src.generate(prompt, 6)
