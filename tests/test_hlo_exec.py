@@ -97,3 +97,26 @@ ENTRY %main (a: f32[4,6,3], b: f32[3,4,5]) -> f32[4,6,5] {
 """
     got, ref = run_both(text)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_cli_validate_only_and_unsupported(tmp_path, capsys):
+    from spirv_inference_amd import hlo_run
+    p = tmp_path / "m.txt"
+    p.write_text(fixture_text("bert_base"))
+    assert hlo_run.main(["--input", str(p), "--validate-only", "--report", str(tmp_path / "r.json")]) == 0
+    rep = json.loads((tmp_path / "r.json").read_text())
+    assert rep["status"] == "pass" and rep["op_histogram"]["dot"] == 4
+    capsys.readouterr()
+    q = tmp_path / "g.txt"
+    q.write_text(SYNTH.replace("exponential(", "gather("))
+    assert hlo_run.main(["--input", str(q), "--validate-only"]) == 0
+    rep = json.loads(capsys.readouterr().out)
+    assert rep["status"] == "blocked_unsupported_feature" and "gather" in rep["validation"]["reason"]
+
+
+def test_cli_compare_follows_tensor_rs():
+    from spirv_inference_amd.hlo_run import compare
+    c = compare(np.array([1.0, 2.0, 3.0], np.float32), np.array([1.0, 2.5, 3.0, 4.0], np.float32), 0.1)
+    # one value off by 0.5 > eps, plus one missing value
+    assert c["mismatch_count"] == 2 and c["max_abs_error"] == 0.5 and abs(c["max_rel_error"] - 0.2) < 1e-7
+    assert compare(np.zeros(2, np.float32), np.zeros(2, np.float32), 0.0)["mismatch_count"] == 0

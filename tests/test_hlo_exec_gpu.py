@@ -74,3 +74,26 @@ def test_tinyllama_fixture_forward(ctx):
     np.testing.assert_allclose(y, nref, rtol=1e-3, atol=1e-3 * np.abs(nref).max())
     print(f"[hlo] tinyllama fixture on device: {dt * 1e3:.1f} ms (uploads + host walk included)",
           flush=True)
+
+
+def test_cli_runs_fixture_with_reference_flags(tmp_path):
+    """hlo_run with main.rs's flags: --inputs-f32 list, --output-f32, --expected-f32, --epsilon."""
+    from spirv_inference_amd import hlo_run
+    text = fixture_text("bert_base")
+    (tmp_path / "m.txt").write_text(text)
+    ops = X.parse_hlo_text(text)
+    params = seeded_params(ops)
+    paths = []
+    for i, p in enumerate(params):
+        paths.append(tmp_path / f"p{i:03d}.raw.f32")
+        p.astype("<f4").tofile(paths[-1])
+    eval_numpy(ops, params).astype("<f4").tofile(tmp_path / "want.raw.f32")
+    rc = hlo_run.main(["--input", str(tmp_path / "m.txt"), "--run", "--inputs-f32",
+                       ",".join(map(str, paths)), "--output-f32", str(tmp_path / "out.raw.f32"),
+                       "--expected-f32", str(tmp_path / "want.raw.f32"), "--epsilon", "1e-3",
+                       "--report", str(tmp_path / "r.json")])
+    import json
+    rep = json.loads((tmp_path / "r.json").read_text())
+    assert rc == 0 and rep["status"] == "pass", rep["execution"]
+    assert rep["execution"]["device"]["vendor_id"] == 0x1002
+    assert (tmp_path / "out.raw.f32").stat().st_size == 4 * rep["execution"]["output"]["elements"]
