@@ -193,6 +193,14 @@ def test_resnet_pools(ctx, orc):
     push = [32, 112, 112, 64, 56, 56, 3, 3, 2, 2, 1, 1, 1, 32 * 56 * 56 * 64]
     y, r = both(ctx, orc, "hlo_reduce_window_rank4", x, None, push[13], push)
     assert y.tobytes() == r.tobytes()
+    # sum windows with C % 4 == 0 (four-channel path) and a C % 4 != 0 max (per-channel path)
+    for shape, win, kind in (((3, 9, 10, 12), (2, 3, 2, 1, 0, 1), 0), ((2, 9, 9, 6), (3, 3, 2, 2, 1, 1), 1)):
+        n, ih, iw, c = shape
+        wh, ww, sh, sw, pt, pl = win
+        oh, ow = (ih + 2 * pt - wh) // sh + 1, (iw + 2 * pl - ww) // sw + 1
+        push = [n, ih, iw, c, oh, ow, wh, ww, sh, sw, pt, pl, kind, n * oh * ow * c]
+        y, r = both(ctx, orc, "hlo_reduce_window_rank4", rnd(*shape), None, push[13], push)
+        assert y.tobytes() == r.tobytes(), shape
     x = rnd(2, 16, 21, 21)
     push = [2, 16, 21, 21, 11, 11, 3, 3, 2, 2, 1, 1, 1, 2 * 16 * 11 * 11]
     y, r = both(ctx, orc, "max_pool2d", x, None, push[13], push)
