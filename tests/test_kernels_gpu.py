@@ -366,6 +366,37 @@ def test_dot_dma_pipeline(ctx, orc, tile, bt, m, k, n):
     assert_close(y, r, 1e-4, 1e-4, f"dma dot {bt}x{m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("tile,bk", [(1, 32), (1, 16), (2, 32), (2, 16), (3, 32), (3, 16)],
+                         ids=["128x128k32", "128x128k16", "128x64k32", "128x64k16", "64x64k32",
+                              "64x64k16"])
+def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk):
+    """Every double-buffered tile the planner can choose, on a padded 3x3 conv with M/N tails
+    and a residual, a 1x1 conv with K = 64, split-K, and a row-major product with a K tail."""
+    cases = [((2, 9, 32, 3, 20, 1), 0), ((3, 8, 64, 1, 72, 1), 0), ((2, 7, 128, 3, 64, 1), 3)]
+    try:
+        _tune("gemm_dma", -1)
+        _tune("gemm_tile", tile)
+        _tune("gemm_bk", bk)
+        for (n, ih, ic, k, oc, s), splits in cases:
+            _tune("gemm_splits", splits)
+            pad = (k - 1) // 2
+            oh = (ih + 2 * pad - k) // s + 1
+            x = rnd(n, ih, ih, ic)
+            w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+            b, res = rnd(oc, scale=0.01), rnd(n * oh * oh * oc)
+            push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+            y, r = both(ctx, orc, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b,
+                        residual=res, act="relu")
+            assert_close(y, r, 1e-4, 1e-4, f"conv {push[:13]} splits {splits}")
+        _tune("gemm_splits", 0)
+        a, bm = rnd(1, 70, 100), rnd(1, 100, 36, scale=0.1)
+        y, r = both(ctx, orc, "hlo_dot_batched", a, bm, 70 * 36, [1, 70, 100, 36, 70 * 36])
+        assert_close(y, r, 1e-4, 1e-4, "dot 70x100x36")
+    finally:
+        for key in ("gemm_dma", "gemm_tile", "gemm_bk", "gemm_splits"):
+            _tune(key, 0)
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256
