@@ -46,7 +46,14 @@ struct GemmParams {
     int splits;
     int k_per_split;  // multiple of the K tile
     float* partial;   // [splits][batch][M][N] workspace when splits > 1
+    int* counters;    // per-tile arrival counters (zero between launches) when fixup
+    int fixup;        // 1: the last split of a tile sums the partials and applies the epilogue
 };
+
+// The first kSplitCounterBytes of a split-K workspace hold the per-tile arrival counters of
+// the in-kernel fixup; they must be zero when a workspace is first handed out, and every
+// launch leaves them zero again.  The partials follow.
+constexpr size_t kSplitCounterBytes = 65536;
 
 // Launch C = epilogue(A*B) for the problem; picks tile shape and split-K.
 // `workspace`/`workspace_bytes` provide the split-K partials (may be null: no split).

@@ -196,19 +196,25 @@ __device__ __forceinline__ void stamp_in(const Epi& e, int which) {
                blockIdx.x] = wall_clock64();
 }
 
-// One chunk: partial dot products of the CH rows in `b`, the workgroup reduction, and the
-// epilogue for rows rc..rc+CH-1.  `red` is [2][NW][8] floats, alternated by `rsel`.
-template <int J, int CH, int EPI>
-__device__ __forceinline__ void chunk_step(const float4 (&b)[NB], const float4 (&xv)[J], int rc,
-                                           int r1, float* red, int& rsel, Epi& e) {
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    float v[8];
+// A chunk is consumed in two steps so that the registers of `b` can be refilled in between:
+// chunk_dots forms this thread's partial dot products of the CH rows, chunk_reduce does the
+// workgroup reduction and the epilogue for rows rc..rc+CH-1 (`red` is [2][NW][8] floats,
+// alternated by `rsel`).
+template <int J, int CH>
+__device__ __forceinline__ void chunk_dots(const float4 (&b)[NB], const float4 (&xv)[J],
+                                           float (&v)[8]) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = 0.0f;
 #pragma unroll
     for (int i = 0; i < CH; ++i)
 #pragma unroll
         for (int j = 0; j < J; ++j) v[i] += dot4(b[i * J + j], xv[j]);
+}
+
+template <int CH, int EPI>
+__device__ __forceinline__ void chunk_reduce(const float (&v)[8], int rc, int r1, float* red,
+                                             int& rsel, Epi& e) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float w = reduce8(v, lane);
     float* rb = red + rsel * (NW * 8);
     rsel ^= 1;
@@ -262,10 +268,18 @@ __device__ __forceinline__ void chunk_step(const float4 (&b)[NB], const float4 (
     }
 }
 
+template <int J, int CH, int EPI>
+__device__ __forceinline__ void chunk_step(const float4 (&b)[NB], const float4 (&xv)[J], int rc,
+                                           int r1, float* red, int& rsel, Epi& e) {
+    float v[8];
+    chunk_dots<J, CH>(b, xv, v);
+    chunk_reduce<CH, EPI>(v, rc, r1, red, rsel, e);
+}
+
 // Rows [r0, r1) of W (row-major, K4 float4 per row) against the per-thread vector slice xv.
 // On entry b0 holds chunk 0 and, when PRE == 2, b1 holds chunk 1 (issued by the caller,
-// usually before a barrier); chunk c+2 is issued before chunk c is consumed, in three
-// rotating register sets.
+// usually before a barrier); chunk c+3 is issued into a register set as soon as the dot
+// products of chunk c have read it, before chunk c's reduction, in three rotating sets.
 template <int J, int CH, int EPI, int PRE = 2>
 __device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4, int r0, int r1,
                                             const float4 (&xv)[J], float4 (&b0)[NB],
@@ -273,39 +287,47 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4,
                                             int& rsel, Epi& e, const float* zero_row) {
     const int nch = (r1 - r0 + CH - 1) / CH;
     if constexpr (PRE == 1) load_chunk<J, CH>(b1, W, K4, r0 + CH, r1, zero_row);
+    load_chunk<J, CH>(b2, W, K4, r0 + 2 * CH, r1, zero_row);
+    float v[8];
     for (int c = 0; c < nch; c += 3) {
-        load_chunk<J, CH>(b2, W, K4, r0 + (c + 2) * CH, r1, zero_row);
-        chunk_step<J, CH, EPI>(b0, xv, r0 + c * CH, r1, red, rsel, e);
-        if (c + 1 >= nch) break;
+        chunk_dots<J, CH>(b0, xv, v);
         load_chunk<J, CH>(b0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
-        chunk_step<J, CH, EPI>(b1, xv, r0 + (c + 1) * CH, r1, red, rsel, e);
-        if (c + 2 >= nch) break;
+        chunk_reduce<CH, EPI>(v, r0 + c * CH, r1, red, rsel, e);
+        if (c + 1 >= nch) break;
+        chunk_dots<J, CH>(b1, xv, v);
         load_chunk<J, CH>(b1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
-        chunk_step<J, CH, EPI>(b2, xv, r0 + (c + 2) * CH, r1, red, rsel, e);
+        chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
+        if (c + 2 >= nch) break;
+        chunk_dots<J, CH>(b2, xv, v);
+        load_chunk<J, CH>(b2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
+        chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
     }
 }
 
 
-// As stream_rows, with chunks 0, 1 and 2 already issued into c0, c1 and c2; the load of
-// chunk c+3 is issued as soon as chunk c has been consumed.
+// As stream_rows, with chunks 0, 1 and 2 already issued into c0, c1 and c2.
 template <int J, int CH, int EPI>
 __device__ __forceinline__ void stream_rows3(const float* __restrict__ W, int K4, int r0, int r1,
                                              const float4 (&xv)[J], float4 (&c0)[NB],
                                              float4 (&c1)[NB], float4 (&c2)[NB], float* red,
                                              int& rsel, Epi& e, const float* zero_row) {
     const int nch = (r1 - r0 + CH - 1) / CH;
+    float v[8];
     for (int c = 0; c < nch; c += 3) {
-        chunk_step<J, CH, EPI>(c0, xv, r0 + c * CH, r1, red, rsel, e);
-        stamp_in(e, 4 + c);
+        chunk_dots<J, CH>(c0, xv, v);
         load_chunk<J, CH>(c0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
+        chunk_reduce<CH, EPI>(v, r0 + c * CH, r1, red, rsel, e);
+        stamp_in(e, 4 + c);
         if (c + 1 >= nch) break;
-        chunk_step<J, CH, EPI>(c1, xv, r0 + (c + 1) * CH, r1, red, rsel, e);
-        stamp_in(e, 5 + c);
+        chunk_dots<J, CH>(c1, xv, v);
         load_chunk<J, CH>(c1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
+        chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
+        stamp_in(e, 5 + c);
         if (c + 2 >= nch) break;
-        chunk_step<J, CH, EPI>(c2, xv, r0 + (c + 2) * CH, r1, red, rsel, e);
-        stamp_in(e, 6 + c);
+        chunk_dots<J, CH>(c2, xv, v);
         load_chunk<J, CH>(c2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
+        chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
+        stamp_in(e, 6 + c);
     }
 }
 

@@ -25,6 +25,28 @@ namespace {
 using shp::GemmParams;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Device-coherent (agent scope) 16-byte store and load of global memory, as two 8-byte
+// relaxed atomics: data written this way by one workgroup is read correctly by a workgroup
+// on another XCD (whose L2 is not coherent with the writer's) within the same launch.
+#define SHP_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ void st_coh4(float* p, float4 v) {
+    SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)p;
+    __hip_atomic_store(q, (unsigned long long)__float_as_uint(v.x) |
+                              ((unsigned long long)__float_as_uint(v.y) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (unsigned long long)__float_as_uint(v.z) |
+                                  ((unsigned long long)__float_as_uint(v.w) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld_coh4(const float* p) {
+    SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)p;
+    const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long hi =
+        __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
+                       __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
+}
+
 constexpr int KTAB = 1024;  // im2col offset table entries (scalar conv modes)
 
 struct ConvRow {
@@ -74,7 +96,11 @@ __device__ __forceinline__ void conv_k(const GemmParams& p, int k, int amode, in
 // row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.  The tile goes through LDS (Cs, the
 // kernel's tile buffer, free again when this is called), RC rows at a time, so global stores
 // (and residual loads) are 16-byte and row-contiguous.  With split-K the raw sums go to the
-// partial buffer instead and the reduction pass applies the epilogue.
+// partial buffer instead.  Then either a separate reduction pass applies the epilogue, or
+// (p.fixup) the split that completes a tile last does: every split stores its partials with
+// device-coherent stores, waits for them, and counts itself in the tile's arrival counter;
+// the one that sees splits - 1 earlier arrivals sums the partials in split order (the
+// reduction pass's order), applies the epilogue and resets the counter to zero.
 template <int BM, int BN, int WM, int WN, int RC, int CS, int CM>
 __device__ __attribute__((always_inline)) inline void gemm_epilogue(
     const GemmParams& p, const floatx16 (&acc)[BM / WM / 32][BN / WN / 32], float* Cs, int m0,
@@ -126,7 +152,8 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
                 if (row >= p.M || col4 >= p.N) continue;
                 float4 v = *reinterpret_cast<const float4*>(&Cs[rl * CS + cl4]);
                 if (P) {
-                    *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
+                    if (p.fixup) st_coh4(P + (int64_t)row * p.N + col4, v);
+                    else *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
                     continue;
                 }
                 const int64_t ci = (int64_t)row * p.scm + col4;
@@ -168,6 +195,44 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
                 C[ci] = shpd::apply_act(v, p.act, p.alpha);
             }
         }
+    }
+    if (P && p.fixup) {  // the host sets fixup only where the 16-byte path applies to C
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are stored
+        __syncthreads();
+        int* last = reinterpret_cast<int*>(Cs);
+        int* cnt = p.counters + (int64_t)bz * gridDim.x + blockIdx.x;
+        if (tid == 0)
+            *last = __hip_atomic_fetch_add((SHP_GLOBAL int*)cnt, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == p.splits - 1;
+        __syncthreads();
+        if (!*last) return;
+        const float* P0 = p.partial + (int64_t)bz * p.M * p.N;
+        const int64_t sstride = (int64_t)nbatch * p.M * p.N;
+        if (p.bias && col4 < p.N) bv = *reinterpret_cast<const float4*>(p.bias + col4);
+        for (int i = 0; i < BM / RPP; ++i) {
+            const int row = m0 + tid / TPR + RPP * i;
+            if (row >= p.M || col4 >= p.N) continue;
+            const float* pp = P0 + (int64_t)row * p.N + col4;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int s = 0; s < p.splits; ++s) {
+                const float4 q = ld_coh4(pp + s * sstride);
+                v.x += q.x;
+                v.y += q.y;
+                v.z += q.z;
+                v.w += q.w;
+            }
+            const int64_t ci = (int64_t)row * p.scm + col4;
+            float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (R) rv = *reinterpret_cast<const float4*>(R + ci);
+            v.x = shpd::apply_act(v.x + bv.x + rv.x, p.act, p.alpha);
+            v.y = shpd::apply_act(v.y + bv.y + rv.y, p.act, p.alpha);
+            v.z = shpd::apply_act(v.z + bv.z + rv.z, p.act, p.alpha);
+            v.w = shpd::apply_act(v.w + bv.w + rv.w, p.act, p.alpha);
+            *reinterpret_cast<float4*>(C + ci) = v;
+        }
+        if (tid == 0)
+            __hip_atomic_store((SHP_GLOBAL int*)cnt, 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -995,7 +1060,7 @@ size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode
     Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
                         dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4);
     if (pl.splits <= 1) return 0;
-    return (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
+    return kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
 }
 
 size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
@@ -1040,7 +1105,9 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     if (amode == A_CONV_NHWC4 && p.cic % 4 != 0) amode = A_CONV_NHWC;
     Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
                         dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4);
-    size_t need = pl.splits > 1 ? (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float) : 0;
+    size_t need = pl.splits > 1
+                      ? kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float)
+                      : 0;
     if (pl.splits > 1 && (workspace == nullptr || workspace_bytes < need)) {
         pl.splits = 1;
         pl.kps = ((p.K + 31) / 32) * 32;
@@ -1048,16 +1115,24 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     }
     p.splits = pl.splits;
     p.k_per_split = pl.kps;
-    p.partial = pl.splits > 1 ? workspace : nullptr;
+    p.partial = pl.splits > 1 ? workspace + kSplitCounterBytes / sizeof(float) : nullptr;
+    p.counters = pl.splits > 1 ? reinterpret_cast<int*>(workspace) : nullptr;
     TileCfg t = pl.t;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
     if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
+    // in-kernel split-K fixup where the epilogue's 16-byte path holds for every batch of C
+    // and the tile counters fit; the separate reduction pass otherwise
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15) == 0; };
+    p.fixup = pl.splits > 1 && cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 &&
+              (p.N & 3) == 0 && (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
+              (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual)) &&
+              ntiles * nbatch <= (int64_t)(kSplitCounterBytes / sizeof(int));
     dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
     int rc = t.dma ? launch_dma(stream, p, amode, t.bn, grid)
                  : dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
     if (rc) return rc;
     SHP_HIP_CHECK(hipGetLastError());
-    if (p.splits > 1) {
+    if (p.splits > 1 && !p.fixup) {
         int64_t total = (int64_t)p.M * p.N * nbatch;
         unsigned g = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
         if (cmode == C_NCHW)

@@ -7,6 +7,7 @@
 // kernel names (kernels.rs:12-238).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -14,6 +15,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gemm.h"
 #include "runtime.h"
 
 namespace shp {
@@ -97,6 +99,8 @@ int Ctx::ensure_workspace(size_t bytes) {
     }
     SHP_HIP_CHECK(hipMalloc((void**)&workspace, bytes));
     workspace_bytes = bytes;
+    // the split-K tile counters at its start must begin at zero (launches keep them zero)
+    SHP_HIP_CHECK(hipMemset(workspace, 0, std::min(bytes, kSplitCounterBytes)));
     return SHP_OK;
 }
 

@@ -397,6 +397,34 @@ def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk):
             _tune(key, 0)
 
 
+@pytest.mark.parametrize("splits", [2, 3, 6])
+def test_splitk_in_kernel_fixup(ctx, orc, gemm_workspace, splits):
+    """Split-K where the last split of each tile reduces the partials and applies the
+    epilogue: three launches in a row (the tile counters must be back at zero after each),
+    a batched product (one counter per batch and tile), and N % 4 != 0, which takes the
+    separate reduction pass."""
+    n, ih, ic, oc = 2, 7, 128, 64
+    x = rnd(n, ih, ih, ic)
+    w = rnd(3, 3, ic, oc, scale=float(np.sqrt(2.0 / (9 * ic))))
+    b, res = rnd(oc, scale=0.01), rnd(n * ih * ih * oc)
+    push = [n, ih, ih, ic, 3, 3, oc, ih, ih, 1, 1, 1, 1, n * ih * ih * oc]
+    r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res, act="relu")
+    try:
+        _tune("gemm_splits", splits)
+        for rep in range(3):
+            y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res,
+                    act="relu")
+            assert_close(y, r, 1e-4, 1e-4, f"split-K conv, launch {rep}")
+        for bt, m, nn in ((3, 40, 36), (1, 40, 30)):
+            a, bm = rnd(bt, m, 768), rnd(bt, 768, nn, scale=0.1)
+            q = [bt, m, 768, nn, bt * m * nn]
+            y = hip(ctx, "hlo_dot_batched", a, bm, bt * m * nn, q)
+            assert_close(y, orc.run("hlo_dot_batched", a, bm, bt * m * nn, q), 1e-4, 1e-4,
+                         f"split-K dot {bt}x{m}x768x{nn}")
+    finally:
+        _tune("gemm_splits", 0)
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256
