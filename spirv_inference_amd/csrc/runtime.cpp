@@ -259,6 +259,13 @@ int shp_sync(shp_ctx* ctx) {
     return SHP_OK;
 }
 
+// Internal tuning hook for experiments (not part of include/spirv_hip.h): grow the context's
+// split-K workspace so forced split counts are not clamped by it.
+int shp_reserve_workspace(shp_ctx* ctx, uint64_t bytes) {
+    if (!ctx) return fail(SHP_ERR_INVALID, "shp_reserve_workspace: null ctx");
+    return reinterpret_cast<Ctx*>(ctx)->ensure_workspace((size_t)bytes);
+}
+
 int shp_fill_random(shp_ctx* ctx, float* dptr, uint64_t n, uint64_t seed, uint64_t tensor_id,
                     int32_t kind, float lo, float hi) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_fill_random: null ctx");

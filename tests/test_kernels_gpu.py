@@ -366,17 +366,21 @@ def test_dot_dma_pipeline(ctx, orc, tile, bt, m, k, n):
     assert_close(y, r, 1e-4, 1e-4, f"dma dot {bt}x{m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("pg", [1, 2], ids=["prefetch1", "prefetch2"])
 @pytest.mark.parametrize("tile,bk", [(1, 32), (1, 16), (2, 32), (2, 16), (3, 32), (3, 16)],
                          ids=["128x128k32", "128x128k16", "128x64k32", "128x64k16", "64x64k32",
                               "64x64k16"])
-def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk):
-    """Every double-buffered tile the planner can choose, on a padded 3x3 conv with M/N tails
-    and a residual, a 1x1 conv with K = 64, split-K, and a row-major product with a K tail."""
-    cases = [((2, 9, 32, 3, 20, 1), 0), ((3, 8, 64, 1, 72, 1), 0), ((2, 7, 128, 3, 64, 1), 3)]
+def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk, pg):
+    """Every double-buffered tile the planner can choose, at both global prefetch depths, on
+    a padded 3x3 conv with M/N tails and a residual (odd K-tile count), 1x1 convs with one and
+    two K tiles, split-K, and a row-major product with a K tail."""
+    cases = [((2, 9, 32, 3, 20, 1), 0), ((3, 8, 64, 1, 72, 1), 0), ((2, 6, 16, 1, 24, 1), 0),
+             ((2, 7, 128, 3, 64, 1), 3)]
     try:
         _tune("gemm_dma", -1)
         _tune("gemm_tile", tile)
         _tune("gemm_bk", bk)
+        _tune("gemm_pg", pg)
         for (n, ih, ic, k, oc, s), splits in cases:
             _tune("gemm_splits", splits)
             pad = (k - 1) // 2
@@ -393,7 +397,7 @@ def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk):
         y, r = both(ctx, orc, "hlo_dot_batched", a, bm, 70 * 36, [1, 70, 100, 36, 70 * 36])
         assert_close(y, r, 1e-4, 1e-4, "dot 70x100x36")
     finally:
-        for key in ("gemm_dma", "gemm_tile", "gemm_bk", "gemm_splits"):
+        for key in ("gemm_dma", "gemm_tile", "gemm_bk", "gemm_splits", "gemm_pg"):
             _tune(key, 0)
 
 
