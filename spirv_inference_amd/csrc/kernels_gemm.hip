@@ -1206,11 +1206,11 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     p.partial = pl.splits > 1 ? workspace + kSplitCounterBytes / sizeof(float) : nullptr;
     p.counters = pl.splits > 1 ? reinterpret_cast<int*>(workspace) : nullptr;
     TileCfg t = pl.t;
-    // Two-deep prefetch for the split-K 64x64 / K-tile 32 plans of the hot operand forms:
-    // 4-7 % faster on the ResNet-50 K = 1024..2304 layers (MI355X sweeps), ~2 % slower
-    // on some short single-split loops.
+    // Two-deep prefetch for the split-K 64x64 / K-tile 32 plans of NHWC convolutions: 4-7 %
+    // faster on the ResNet-50 K = 1024..2304 layers (MI355X sweeps), ~2 % slower on some
+    // short single-split loops, and 3x slower on the M = 32 row-major FC (one tile row).
     if (!t.dma && t.bm == 64 && t.bn == 64 && t.bk == 32 && pl.splits > 1 &&
-        combo_is_hot(amode, bmode, cmode))
+        amode == A_CONV_NHWC4 && combo_is_hot(amode, bmode, cmode))
         t.pg = 2;
     if (g_force_pg) t.pg = g_force_pg;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
