@@ -67,6 +67,19 @@ def measured_conv_traffic(batch: int):
     return None
 
 
+def measured_decode_traffic(n_prompt: int, n_new: int):
+    """HBM bytes per token of the persistent decode from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/tinyllama_decode_persistent.md: 32-token prompt, 20 new
+    tokens), or None for another workload."""
+    path = os.path.join(ROOT, "profiles", "tinyllama_decode_persistent.md")
+    if (n_prompt, n_new) != (32, 20) or not os.path.exists(path):
+        return None
+    for ln in open(path):
+        if ln.startswith("hbm_bytes_per_token"):
+            return float(ln.split("=")[1])
+    return None
+
+
 def bench_resnet(ctx, steps: int, warmup: int, batch: int):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
@@ -345,7 +358,12 @@ def main() -> int:
             "ms_per_token": round(dec["ms_per_token"], 4),
             "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(dec["achieved_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                         "frac": round(dec["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                         "traffic": (measured_decode_traffic(args.prompt_tokens, args.decode_tokens)
+                                     if dec["engine"] == "persistent" else None),
+                         "traffic_unit": "HBM bytes per token (rocprofv3 FETCH_SIZE x2.0 + "
+                                         "WRITE_SIZE x1.0, scaled by a 256 MiB copy; "
+                                         "profiles/tinyllama_decode_persistent.md)",
                          "bytes_per_token": dec["bytes_per_token"]},
             "tokens": dec["tokens"],
             "engine": dec["engine"],

@@ -78,6 +78,9 @@ def main() -> int:
                     help="load a Hugging Face safetensors checkpoint (one file or shards)")
     ap.add_argument("--profile-phases", type=int, default=0, metavar="N",
                     help="after the timed runs, stamp-profile N tokens of the persistent engine")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0, metavar="MB",
+                    help="finish with a plain device copy of MB MiB (scales rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     rng = np.random.default_rng(args.prompt_seed)
     prompt = [int(t) for t in rng.integers(0, TINYLLAMA["vocab"], args.prompt_tokens)]
@@ -109,6 +112,14 @@ def main() -> int:
                 lm.step(t)
             print(phase_profile(lm, args.profile_phases), flush=True)
         lm.close()
+        if args.copy_calibration_mb > 0:
+            n = args.copy_calibration_mb * (1 << 20) // 4
+            src, dst = ctx.empty(n), ctx.empty(n)
+            ctx.fill_random(src, 9, 0, "uniform", 0.0, 1.0)
+            ctx.launch("reshape", src, None, dst, [n])
+            ctx.sync()
+            src.free()
+            dst.free()
     return 0
 
 
