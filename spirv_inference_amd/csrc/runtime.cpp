@@ -59,6 +59,8 @@ const KernelEntry* find_kernel(const char* name) {
     return nullptr;
 }
 
+size_t gemm_workspace_for_kernel(const char* name, const int32_t* push, size_t n_push);
+
 int launch_kernel(hipStream_t stream, const char* name, const void* in0, const void* in1,
                   void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
                   const shp_epilogue* epi, float* workspace, size_t workspace_bytes) {
@@ -107,6 +109,19 @@ int Ctx::ensure_workspace(size_t bytes) {
 int Ctx::launch(const char* name, const void* in0, const void* in1, void* out,
                 const int32_t* push, size_t n_push, uint64_t out_elems, const shp_epilogue* epi) {
     if (device >= 0) SHP_HIP_CHECK(hipSetDevice(device));
+    // A dense kernel's split-K partials live in the context workspace: grow it on the first
+    // launch that asks for more, except while the stream is being captured into a graph
+    // (no allocation there; such a launch runs without splitting K).  Model graphs size it
+    // before they capture.
+    const size_t need = name ? gemm_workspace_for_kernel(name, push, n_push) : 0;
+    if (need > workspace_bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        SHP_HIP_CHECK(hipStreamIsCapturing(stream, &cs));
+        if (cs == hipStreamCaptureStatusNone) {
+            int rc = ensure_workspace(need);
+            if (rc) return rc;
+        }
+    }
     Timer* t = nullptr;
     if (timing) {
         if (timer_used == timers.size()) {

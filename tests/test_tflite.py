@@ -1,0 +1,171 @@
+"""TFLite front end on the CPU: FlatBuffer reading / writing, option decoding with the
+reference's defaults, topological order, unsupported-op and quantized-tensor detection
+(source/tflite_loader/src/{model,op_decoder,graph,scheduler}.rs)."""
+import struct
+
+import numpy as np
+import pytest
+
+from spirv_inference_amd import tflite as T
+
+
+def logistic_model() -> bytes:
+    """The model fixtures/make_synthetic_logistic_tflite.py:20-83 writes: tensors input /
+    output [1, 8], one LOGISTIC operator (deprecated and new builtin code 14), version 3."""
+    w = T.TfliteWriter("synthetic float32 logistic model for cuda-spirv loader smoke test")
+    i = w.tensor("input", [1, 8])
+    o = w.tensor("output", [1, 8])
+    w.inputs, w.outputs = [i], [o]
+    w.op("LOGISTIC", [i], [o])
+    return w.finish()
+
+
+def test_logistic_fixture_fields():
+    data = logistic_model()
+    assert data[4:8] == b"TFL3"
+    m = T.parse_model(data, "logistic.tflite")
+    assert m.version == 3
+    assert m.description.startswith("synthetic float32 logistic model")
+    assert [(t.name, t.shape, t.tensor_type) for t in m.tensors] == [
+        ("input", [1, 8], "Float32"), ("output", [1, 8], "Float32")]
+    assert (m.inputs, m.outputs) == ([0], [1])
+    assert [(o.builtin, o.code, o.inputs, o.outputs) for o in m.operators] == [
+        ("LOGISTIC", 14, [0], [1])]
+    assert m.op_histogram == {"LOGISTIC": 1} and not m.unsupported_ops
+    assert T.validate_supported_graph(m)["status"] == "pass"
+    assert T.topological_order(m) == [0]
+    s = m.summary()
+    assert s["buffers"][0]["data_len"] == 0 and s["operators"][0]["builtin_options_table_pos"] is None
+
+
+def test_identifier_and_size_checks():
+    with pytest.raises(ValueError, match="too small"):
+        T.parse_model(b"TFL3")
+    bad = bytearray(logistic_model())
+    bad[4:8] = b"XXXX"
+    with pytest.raises(ValueError, match="TFL3"):
+        T.parse_model(bytes(bad))
+    truncated = logistic_model()[:40]
+    with pytest.raises(ValueError):
+        T.parse_model(truncated)
+
+
+def test_constant_buffers_roundtrip():
+    w = T.TfliteWriter()
+    x = w.tensor("x", [1, 4, 4, 3])
+    data = np.arange(2 * 3 * 3 * 3, dtype=np.float32) * 0.5
+    k = w.tensor("k", [2, 3, 3, 3], data)
+    y = w.tensor("y", [1, 4, 4, 2])
+    w.inputs, w.outputs = [x], [y]
+    w.op("CONV_2D", [x, k, -1], [y], "Conv2DOptions",
+         {0: ("b", 1), 1: ("i", 2), 2: ("i", 3), 3: ("b", 3), 4: ("i", 1), 5: ("i", 1)})
+    m = T.parse_model(w.finish())
+    buf = m.buffers[m.tensors[1].buffer]
+    np.testing.assert_array_equal(np.frombuffer(buf.data, "<f4"), data)
+    assert buf.data_offset % 16 == 0
+    o = T.decode_options(m.operators[0])
+    assert o == {"kind": "conv2d", "padding": "valid", "stride_w": 2, "stride_h": 3,
+                 "fused_activation": "relu6", "dilation_w_factor": 1, "dilation_h_factor": 1}
+    assert m.operators[0].options_type == T.OPTIONS_TYPE["Conv2DOptions"]
+    assert m.operators[0].inputs == [0, 1, -1]
+
+
+@pytest.mark.parametrize("builtin,kind,expected", [
+    ("CONV_2D", "Conv2DOptions", {"padding": "same", "stride_w": 1, "stride_h": 1,
+                                  "fused_activation": "none", "dilation_w_factor": 1,
+                                  "dilation_h_factor": 1}),
+    ("DEPTHWISE_CONV_2D", "DepthwiseConv2DOptions", {"depth_multiplier": 1, "stride_w": 1}),
+    ("MAX_POOL_2D", "Pool2DOptions", {"filter_w": 1, "filter_h": 1, "padding": "same"}),
+    ("SOFTMAX", "SoftmaxOptions", {"beta": 1.0}),
+    ("LEAKY_RELU", "LeakyReluOptions", {"alpha": pytest.approx(0.2)}),
+    ("CONCATENATION", "ConcatenationOptions", {"axis": 0, "fused_activation": "none"}),
+    ("MEAN", "ReducerOptions", {"keep_dims": False}),
+])
+def test_option_defaults(builtin, kind, expected):
+    """Absent option fields take op_decoder.rs's defaults (stride 1, dilation 1, beta 1.0,
+    leaky alpha 0.2, SAME padding, no activation)."""
+    w = T.TfliteWriter()
+    a = w.tensor("a", [1, 2, 2, 2])
+    b = w.tensor("b", [1, 2, 2, 2])
+    w.inputs, w.outputs = [a], [b]
+    w.op(builtin, [a], [b], kind, {})
+    o = T.decode_options(T.parse_model(w.finish()).operators[0])
+    for k, v in expected.items():
+        assert o[k] == v, (k, o)
+
+
+def test_resize_bilinear_reads_schema_fields():
+    w = T.TfliteWriter()
+    a = w.tensor("a", [1, 2, 2, 1])
+    b = w.tensor("b", [1, 4, 4, 1])
+    w.inputs, w.outputs = [a], [b]
+    w.op("RESIZE_BILINEAR", [a], [b], "ResizeBilinearOptions", {2: ("B", 1), 3: ("B", 0)})
+    o = T.decode_options(T.parse_model(w.finish()).operators[0])
+    assert o == {"kind": "resize", "align_corners": True, "half_pixel_centers": False}
+
+
+def _two_op_model(first_consumer: bool) -> T.TfliteModel:
+    w = T.TfliteWriter()
+    x = w.tensor("x", [4])
+    h = w.tensor("h", [4])
+    y = w.tensor("y", [4])
+    w.inputs, w.outputs = [x], [y]
+    if first_consumer:
+        w.op("EXP", [h], [y])
+        w.op("ABS", [x], [h])
+    else:
+        w.op("ABS", [x], [h])
+        w.op("EXP", [h], [y])
+    return T.parse_model(w.finish())
+
+
+def test_topological_order():
+    """scheduler.rs:1684-1730: a model already in ready order keeps it; otherwise producers
+    come first; two producers of one tensor are an error."""
+    assert T.topological_order(_two_op_model(False)) == [0, 1]
+    assert T.topological_order(_two_op_model(True)) == [1, 0]
+    w = T.TfliteWriter()
+    x = w.tensor("x", [4])
+    y = w.tensor("y", [4])
+    w.inputs, w.outputs = [x], [y]
+    w.op("ABS", [x], [y])
+    w.op("EXP", [x], [y])
+    with pytest.raises(ValueError, match="multiple producers"):
+        T.topological_order(T.parse_model(w.finish()))
+
+
+def test_unsupported_and_quantized_detection():
+    """model.rs:334-350 / graph.rs:5-21: an operator code outside the recognised table and a
+    non-float, non-int32 tensor each block the graph."""
+    w = T.TfliteWriter()
+    x = w.tensor("x", [4])
+    y = w.tensor("y", [4], ttype=3)  # UInt8
+    w.inputs, w.outputs = [x], [y]
+    w.op("ABS", [x], [y])
+    data = bytearray(w.finish())
+    m = T.parse_model(bytes(data))
+    assert m.quantized_tensors == ["y:UInt8"]
+    with pytest.raises(ValueError, match="quantized"):
+        T.validate_supported_graph(m)
+    # RELU (code 19) is not in the reference's operator table
+    w = T.TfliteWriter()
+    x = w.tensor("x", [4])
+    y = w.tensor("y", [4])
+    w.inputs, w.outputs = [x], [y]
+    w.op("ABS", [x], [y])
+    w.opcodes[0] = 19
+    m = T.parse_model(w.finish())
+    assert m.unsupported_ops == ["operator 0: UNKNOWN_19"]
+    with pytest.raises(ValueError, match="unsupported TFLite ops"):
+        T.validate_supported_graph(m)
+
+
+def test_default_input_and_top1():
+    v = T.default_input(8)
+    np.testing.assert_array_equal(v, (np.arange(8) - 4.0) * 0.25)
+    # the last maximum wins (Rust max_by), and a 1001-class head drops its background class
+    assert T.top1(np.array([1.0, 3.0, 3.0, 2.0]))["model_class"] == 2
+    h = np.zeros(1001, np.float32)
+    h[0], h[7] = 9.0, 5.0
+    t = T.top1(h)
+    assert (t["model_class"], t["class"]) == (7, 6)
