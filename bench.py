@@ -6,10 +6,14 @@ graph, with TinyLlama-1.1B fp32 greedy decode tok/s an
 roofline fractions reported beside it.  Synthetic seeded inputs and random-init weights,
 generated on the device; inputs are resident in HBM before the timed region starts.
 
-Timed region: K forward passes replayed from one hipGraph capture of the step; host wall
-clock around them gives value and ms_per_step.  Profiled region: the same K passes launched
-eagerly with a hipEvent pair around every kernel on the context stream; those per-kernel
-durations give the roofline of the dominant kernel (the MFMA implicit-GEMM convolution).  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
+Timed region: K steps of 32 images, each run as `--streams` concurrent sub-batches (default two
+of 16: one context, HIP stream and hipGraph capture per sub-batch, identical weights from the same
+seed, inputs the consecutive slices of the b32 input), replayed K times; host wall clock around
+them gives value and ms_per_step.  The concurrent chains fill the CUs that one chain's tile-count
+tails leave idle.  The single-stream b32 graph replay is timed too and reported beside it.
+Profiled region: K b32 passes launched eagerly on one stream with a hipEvent pair around every
+kernel; those per-kernel durations give the roofline of the dominant kernel (the MFMA
+implicit-GEMM convolution), free of overlap between launches.  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
 a bounded sample of the same workload on this box's host cores.
 
 Prints ONE JSON line.  --gpus N > 1 exits with an explanation (single-GPU build).
@@ -80,7 +84,46 @@ def measured_decode_traffic(n_prompt: int, n_new: int):
     return None
 
 
-def bench_resnet(ctx, steps: int, warmup: int, batch: int):
+def time_split_streams(ctx, m, steps: int, warmup: int, batch: int, streams: int):
+    """K steps of the b{batch} forward as `streams` concurrent sub-batches: one context (its
+    own HIP stream and split-K workspace) and one hipGraph per sub-batch, the same weights (same
+    seed), inputs the consecutive slices of m's input.  Returns (img/s, ms per step, top-1)."""
+    from spirv_inference_amd import Context
+    from spirv_inference_amd.models import Model
+    sub = batch // streams
+    x = m.input(0).download().reshape(batch, -1)
+    ctxs = [ctx] + [Context("any") for _ in range(streams - 1)]
+    parts = []
+    try:
+        for i, c in enumerate(ctxs):
+            part = Model(c, "resnet50_v1_5", sub, seed=2)
+            parts.append(part)
+            part.input(0).upload(x[i * sub:(i + 1) * sub])
+            part.use_graph(True)
+        for _ in range(max(warmup, 1)):
+            for part in parts:
+                part.run()
+        for c in ctxs:
+            c.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            for part in parts:
+                part.run()
+        for c in ctxs:
+            c.sync()
+        elapsed = time.perf_counter() - t0
+        top1 = []
+        for part in parts:
+            top1 += [int(i) for i in np.argmax(part.output(1).download().reshape(sub, -1), axis=1)]
+        return batch * steps / elapsed, elapsed / steps * 1e3, top1
+    finally:
+        for part in parts:
+            part.close()
+        for c in ctxs[1:]:
+            c.close()
+
+
+def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
     flops, wbytes = m.work()
@@ -125,7 +168,11 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int):
         conv_ms_per_step=conv_ms / steps, conv_launches=conv_n,
         conv_avg_launch_ms=conv_ms / max(conv_n, 1), achieved_tflops=achieved,
         per_kernel_ms={k: v[0] / steps for k, v in sorted(rep.items())}, top1=top1,
-        weight_bytes=wbytes)
+        weight_bytes=wbytes, streams=1, single_img_s=batch * steps / elapsed,
+        single_ms_per_step=elapsed / steps * 1e3, split_top1=None)
+    if streams > 1 and batch % streams == 0:
+        img_s, ms, split_top1 = time_split_streams(ctx, m, steps, warmup, batch, streams)
+        res.update(img_s=img_s, ms_per_step=ms, streams=streams, split_top1=split_top1)
     m.close()
     return res
 
@@ -243,6 +290,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--streams", type=int, default=2,
+                    help="concurrent sub-batches (streams) a step is split into; 1 = one b32 chain")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--prompt-tokens", type=int, default=32)
     ap.add_argument("--cpu-sample", type=int, default=32, help="images for the CPU baseline")
@@ -263,7 +312,11 @@ def main() -> int:
     from spirv_inference_amd import Context
     ctx = Context("any")
     log(f"device {ctx.device_name}")
-    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch)
+    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.streams)
+    if rn["streams"] > 1:
+        log(f"resnet50 b{args.batch} as {rn['streams']} concurrent sub-batches: "
+            f"{rn['img_s']:.1f} img/s (single stream {rn['single_img_s']:.1f}); top-1 identical "
+            f"to the b{args.batch} chain: {rn['split_top1'] == rn['top1']}")
     log(f"resnet50 b{args.batch}: {rn['img_s']:.1f} img/s, {rn['ms_per_step']:.3f} ms/step "
         f"(eager+events {rn['eager_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
     configs = {}
@@ -314,6 +367,8 @@ def main() -> int:
                         "reduce_window max-pool, mean pool, dot 2048->1000, softmax), "
                         "He-normal weights with folded BN",
             "global_batch": args.batch,
+            "streams": rn["streams"],
+            "sub_batch": args.batch // rn["streams"],
             "flops_per_img": rn["flops_per_img"],
             "seed": 2,
         },
@@ -339,8 +394,16 @@ def main() -> int:
                       f"top-1 identical to the GPU's: {cpu['top1_match']}",
         },
         "extra": {
-            "timed_region": "hipGraph replay of the whole step, K times, host clock",
-            "profiled_region": "the same K steps launched eagerly with a hipEvent pair per kernel",
+            "timed_region": (f"K steps of {args.batch} images as {rn['streams']} concurrent "
+                             f"sub-batches (one HIP stream + hipGraph each), host clock"
+                             if rn["streams"] > 1 else
+                             "hipGraph replay of the whole step, K times, host clock"),
+            "profiled_region": f"K b{args.batch} steps launched eagerly on one stream with a "
+                               "hipEvent pair per kernel (roofline source)",
+            "single_stream_img_s": round(rn["single_img_s"], 3),
+            "single_stream_ms_per_step": round(rn["single_ms_per_step"], 4),
+            "split_top1_identical": (None if rn["split_top1"] is None
+                                     else rn["split_top1"] == rn["top1"]),
             "eager_ms_per_step": round(rn["eager_ms_per_step"], 4),
             "kernel_ms_per_step": round(rn["kernel_ms_per_step"], 4),
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},
