@@ -715,7 +715,7 @@ __device__ __attribute__((always_inline)) inline void dma_segment(
             dma16(ok ? src : zero, dst);
         } else {
             const float* src = arow[u] + q_kt0;
-            dma16(kin & aok[u] ? src : zero, dst);
+            dma16((kin && aok[u]) ? src : zero, dst);
         }
     };
     auto dma_b = [&](int u, unsigned sb) __attribute__((always_inline)) {

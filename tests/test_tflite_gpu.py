@@ -179,3 +179,74 @@ def test_tflite_run_cli(tmp_path):
     assert all(c["mismatch_count"] == 0 for c in st["cases"])
     dumped = np.fromfile(tmp_path / "d" / "output.raw.f32", "<f4")
     np.testing.assert_allclose(dumped, np.tanh(T.default_input(16)), rtol=1e-5, atol=1e-6)
+
+
+def test_elementwise_graph(ctx):
+    """Every binary and unary lowering, fused activations on ADD and AVERAGE_POOL_2D, RESHAPE
+    views, L2_NORMALIZATION and the 10-class SOFTMAX, chained, against float64 numpy."""
+    shape = [1, 4, 4, 10]
+    x = RNG.uniform(0.5, 2.0, shape).astype(np.float32)
+    c = RNG.uniform(0.5, 2.0, shape).astype(np.float32)
+    ten = np.full(shape, 10.0, np.float32)
+    w = T.TfliteWriter("elementwise")
+    tx = w.tensor("x", shape)
+    tc, tten = w.tensor("c", shape, c), w.tensor("ten", shape, ten)
+    w.inputs = [tx]
+    d = {}
+
+    def op(name, builtin, ins, out_shape=shape, kind=None, opts=None):
+        d[name] = w.tensor(name, out_shape)
+        w.op(builtin, ins, [d[name]], kind, opts or {})
+        return d[name]
+
+    op("t1", "SUB", [tx, tc])
+    op("t2", "MUL", [d["t1"], tc])
+    op("t3", "DIV", [d["t2"], tc])
+    op("t4", "POW", [tx, tc])
+    op("t5", "MINIMUM", [d["t3"], d["t4"]])
+    op("t6", "MAXIMUM", [d["t5"], d["t1"]])
+    op("t7", "ABS", [d["t6"]])
+    op("t8", "NEG", [d["t7"]])
+    op("t9", "EXP", [d["t8"]])
+    op("t10", "LOG", [d["t9"]])
+    op("t11", "SQRT", [d["t4"]])
+    op("t12", "RSQRT", [d["t4"]])
+    op("t13", "TANH", [d["t1"]])
+    op("t14", "LOGISTIC", [d["t13"]])
+    op("t15", "LEAKY_RELU", [d["t1"]], kind="LeakyReluOptions", opts={0: ("f", 0.1)})
+    op("t16", "MUL", [d["t15"], tten])
+    op("t17", "RELU6", [d["t16"]])
+    op("t18", "ADD", [d["t17"], d["t12"]], kind="AddOptions", opts={0: ("b", 3)})
+    op("t19", "ADD", [d["t18"], d["t10"]])
+    op("t20", "ADD", [d["t19"], d["t11"]])
+    op("t21", "ADD", [d["t20"], d["t14"]])
+    op("flat", "RESHAPE", [d["t21"]], [1, 160])
+    op("l2", "L2_NORMALIZATION", [d["flat"]], [1, 160])
+    op("back", "RESHAPE", [d["l2"]])
+    op("pool", "AVERAGE_POOL_2D", [d["back"]], [1, 1, 1, 10], "Pool2DOptions",
+       {0: ("b", 1), 1: ("i", 4), 2: ("i", 4), 3: ("i", 4), 4: ("i", 4), 5: ("b", 1)})
+    op("y", "SOFTMAX", [d["pool"]], [1, 10], "SoftmaxOptions", {0: ("f", 1.0)})
+    w.outputs = [d["y"]]
+    m = T.parse_model(w.finish())
+    print("[gpu] tflite elementwise graph", flush=True)
+    rep, got = T.run_model(ctx, m, x)
+
+    X, Cc = x.astype(np.float64), c.astype(np.float64)
+    t1 = X - Cc
+    t3 = t1 * Cc / Cc
+    t4 = X ** Cc
+    t6 = np.maximum(np.minimum(t3, t4), t1)
+    t10 = np.log(np.exp(-np.abs(t6)))
+    t11, t12 = np.sqrt(t4), 1.0 / np.sqrt(t4)
+    t14 = 1.0 / (1.0 + np.exp(-np.tanh(t1)))
+    t17 = np.clip(np.where(t1 >= 0, t1, 0.1 * t1) * 10.0, 0.0, 6.0)
+    t18 = np.clip(t17 + t12, 0.0, 6.0)
+    t21 = t18 + t10 + t11 + t14
+    l2 = t21 / np.sqrt((t21 ** 2).sum())
+    pool = np.maximum(l2.reshape(16, 10).mean(axis=0), 0.0)
+    e = np.exp(pool - pool.max())
+    assert_close(got, e / e.sum(), 1e-4, 1e-4, "elementwise graph")
+    kernels = {d_["kernel"] for o in rep["ops"] for d_ in o["dispatches"]}
+    assert {"sub", "mul", "div", "pow", "min", "max", "abs", "neg", "exp", "log", "sqrt",
+            "rsqrt", "tanh", "sigmoid", "leaky_relu", "relu6", "add", "l2_normalization",
+            "global_avg_pool_nhwc", "relu", "softmax10"} <= kernels
