@@ -6,11 +6,13 @@ graph, with TinyLlama-1.1B fp32 greedy decode tok/s an
 roofline fractions reported beside it.  Synthetic seeded inputs and random-init weights,
 generated on the device; inputs are resident in HBM before the timed region starts.
 
-Timed region: K steps of 32 images, each run as `--streams` concurrent sub-batches (default two
-of 16: one context, HIP stream and hipGraph capture per sub-batch, identical weights from the same
-seed, inputs the consecutive slices of the b32 input), replayed K times; host wall clock around
-them gives value and ms_per_step.  The concurrent chains fill the CUs that one chain's tile-count
-tails leave idle.  The single-stream b32 graph replay is timed too and reported beside it.
+Timed region: K steps of 32 images over `--streams` contexts (default two; one HIP stream,
+split-K workspace and hipGraph capture each, identical weights from the same seed).  With
+`--overlap steps` (default) whole b32 steps are dealt round-robin over the streams, so two
+independent batches are in flight at once; with `--overlap split` each step runs as concurrent
+sub-batches (two of 16).  Host wall clock around the K steps gives value and ms_per_step.  The
+concurrent chains fill the CUs that one chain's tile-count tails and per-tile prologue/epilogue
+phases leave idle.  The single-stream b32 graph replay is timed too and reported beside it.
 Profiled region: K b32 passes launched eagerly on one stream with a hipEvent pair around every
 kernel; those per-kernel durations give the roofline of the dominant kernel (the MFMA
 implicit-GEMM convolution), free of overlap between launches.  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
@@ -123,7 +125,42 @@ def time_split_streams(ctx, m, steps: int, warmup: int, batch: int, streams: int
             c.close()
 
 
-def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1):
+def time_alternating_steps(ctx, m, steps: int, warmup: int, batch: int, streams: int):
+    """K b{batch} steps dealt round-robin over `streams` contexts (one HIP stream and hipGraph
+    each, same weights and input), so consecutive steps overlap.  Returns (img/s, ms/step, top-1)."""
+    from spirv_inference_amd import Context
+    from spirv_inference_amd.models import Model
+    x = m.input(0).download()
+    ctxs = [ctx] + [Context("any") for _ in range(streams - 1)]
+    parts = []
+    try:
+        for c in ctxs:
+            part = Model(c, "resnet50_v1_5", batch, seed=2)
+            parts.append(part)
+            part.input(0).upload(x)
+            part.use_graph(True)
+        for _ in range(max(warmup, 1)):
+            for part in parts:
+                part.run()
+        for c in ctxs:
+            c.sync()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            parts[k % streams].run()
+        for c in ctxs:
+            c.sync()
+        elapsed = time.perf_counter() - t0
+        top1 = [int(i) for i in np.argmax(parts[-1].output(1).download().reshape(batch, -1), axis=1)]
+        return batch * steps / elapsed, elapsed / steps * 1e3, top1
+    finally:
+        for part in parts:
+            part.close()
+        for c in ctxs[1:]:
+            c.close()
+
+
+def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1,
+                 overlap: str = "split"):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
     flops, wbytes = m.work()
@@ -170,8 +207,9 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1):
         per_kernel_ms={k: v[0] / steps for k, v in sorted(rep.items())}, top1=top1,
         weight_bytes=wbytes, streams=1, single_img_s=batch * steps / elapsed,
         single_ms_per_step=elapsed / steps * 1e3, split_top1=None)
-    if streams > 1 and batch % streams == 0:
-        img_s, ms, split_top1 = time_split_streams(ctx, m, steps, warmup, batch, streams)
+    if streams > 1 and (overlap == "steps" or batch % streams == 0):
+        fn = time_split_streams if overlap == "split" else time_alternating_steps
+        img_s, ms, split_top1 = fn(ctx, m, steps, warmup, batch, streams)
         res.update(img_s=img_s, ms_per_step=ms, streams=streams, split_top1=split_top1)
     m.close()
     return res
@@ -292,6 +330,9 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--streams", type=int, default=2,
                     help="concurrent sub-batches (streams) a step is split into; 1 = one b32 chain")
+    ap.add_argument("--overlap", choices=("split", "steps"), default="steps",
+                    help="split: each step as concurrent sub-batches; steps: whole b32 steps "
+                         "dealt round-robin over the streams")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--prompt-tokens", type=int, default=32)
     ap.add_argument("--cpu-sample", type=int, default=32, help="images for the CPU baseline")
@@ -312,11 +353,13 @@ def main() -> int:
     from spirv_inference_amd import Context
     ctx = Context("any")
     log(f"device {ctx.device_name}")
-    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.streams)
+    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.streams, args.overlap)
     if rn["streams"] > 1:
-        log(f"resnet50 b{args.batch} as {rn['streams']} concurrent sub-batches: "
+        how = ("b%d steps round-robin over" % args.batch if args.overlap == "steps"
+               else "sub-batches on")
+        log(f"resnet50 b{args.batch}, {how} {rn['streams']} concurrent streams: "
             f"{rn['img_s']:.1f} img/s (single stream {rn['single_img_s']:.1f}); top-1 identical "
-            f"to the b{args.batch} chain: {rn['split_top1'] == rn['top1']}")
+            f"to the single-stream chain: {rn['split_top1'] == rn['top1']}")
     log(f"resnet50 b{args.batch}: {rn['img_s']:.1f} img/s, {rn['ms_per_step']:.3f} ms/step "
         f"(eager+events {rn['eager_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
     configs = {}
@@ -368,7 +411,9 @@ def main() -> int:
                         "He-normal weights with folded BN",
             "global_batch": args.batch,
             "streams": rn["streams"],
-            "sub_batch": args.batch // rn["streams"],
+            "overlap": args.overlap if rn["streams"] > 1 else None,
+            "batch_per_launch": (args.batch // rn["streams"]
+                                 if rn["streams"] > 1 and args.overlap == "split" else args.batch),
             "flops_per_img": rn["flops_per_img"],
             "seed": 2,
         },
@@ -394,8 +439,11 @@ def main() -> int:
                       f"top-1 identical to the GPU's: {cpu['top1_match']}",
         },
         "extra": {
-            "timed_region": (f"K steps of {args.batch} images as {rn['streams']} concurrent "
-                             f"sub-batches (one HIP stream + hipGraph each), host clock"
+            "timed_region": ((f"K b{args.batch} steps dealt round-robin over {rn['streams']} "
+                              "HIP streams (one hipGraph each, two steps in flight), host clock"
+                              if args.overlap == "steps" else
+                              f"K steps of {args.batch} images as {rn['streams']} concurrent "
+                              "sub-batches (one HIP stream + hipGraph each), host clock")
                              if rn["streams"] > 1 else
                              "hipGraph replay of the whole step, K times, host clock"),
             "profiled_region": f"K b{args.batch} steps launched eagerly on one stream with a "
