@@ -6,10 +6,10 @@ graph, with TinyLlama-1.1B fp32 greedy decode tok/s an
 roofline fractions reported beside it.  Synthetic seeded inputs and random-init weights,
 generated on the device; inputs are resident in HBM before the timed region starts.
 
-Timed region: K steps of 32 images over `--streams` contexts (default two; one HIP stream,
+Timed region: K steps of 32 images over `--streams` contexts (default three; one HIP stream,
 split-K workspace and hipGraph capture each, identical weights from the same seed).  With
-`--overlap steps` (default) whole b32 steps are dealt round-robin over the streams, so two
-independent batches are in flight at once; with `--overlap split` each step runs as concurrent
+`--overlap steps` (default) whole b32 steps are dealt round-robin over the streams, so up to
+three independent batches are in flight at once; with `--overlap split` each step runs as concurrent
 sub-batches (two of 16).  Host wall clock around the K steps gives value and ms_per_step.  The
 concurrent chains fill the CUs that one chain's tile-count tails and per-tile prologue/epilogue
 phases leave idle.  The single-stream b32 graph replay is timed too and reported beside it.
@@ -328,7 +328,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=32)
-    ap.add_argument("--streams", type=int, default=2,
+    ap.add_argument("--streams", type=int, default=3,
                     help="concurrent sub-batches (streams) a step is split into; 1 = one b32 chain")
     ap.add_argument("--overlap", choices=("split", "steps"), default="steps",
                     help="split: each step as concurrent sub-batches; steps: whole b32 steps "
@@ -440,7 +440,7 @@ def main() -> int:
         },
         "extra": {
             "timed_region": ((f"K b{args.batch} steps dealt round-robin over {rn['streams']} "
-                              "HIP streams (one hipGraph each, two steps in flight), host clock"
+                              f"HIP streams (one hipGraph each, {rn['streams']} steps in flight), host clock"
                               if args.overlap == "steps" else
                               f"K steps of {args.batch} images as {rn['streams']} concurrent "
                               "sub-batches (one HIP stream + hipGraph each), host clock")

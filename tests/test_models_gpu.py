@@ -131,37 +131,40 @@ def test_resnet50_b32_as_concurrent_sub_batches(ctx):
         c2.close()
 
 
-def test_resnet50_b32_steps_overlapped_on_two_streams(ctx):
-    """bench.py's default timed loop: whole b32 steps dealt over two contexts (streams), each
+def test_resnet50_b32_steps_overlapped_on_three_streams(ctx):
+    """bench.py's default timed loop: whole b32 steps dealt over three contexts (streams), each
     replaying its own hipGraph while the other runs.  Both chains hold the same weights and
     input, so every replay on either stream equals the single eager run bit for bit."""
     from spirv_inference_amd import Context
     from spirv_inference_amd.models import Model
-    c2 = Context("any")
+    extra = [Context("any"), Context("any")]
+    ctxs = [ctx] + extra
     parts = []
     try:
-        for c in (ctx, c2):
+        for c in ctxs:
             parts.append(Model(c, "resnet50_v1_5", 32, seed=2))
         x = parts[0].input(0).download()
-        parts[1].input(0).upload(x)
+        for part in parts[1:]:
+            part.input(0).upload(x)
         parts[0].run()
         ctx.sync()
         eager = parts[0].output(1).download()
         for part in parts:
             part.use_graph(True)
-        for k in range(6):
-            print(f"[gpu] overlapped b32 step {k} on stream {k % 2}", flush=True)
-            parts[k % 2].run()
-            if k % 2:
-                ctx.sync()
-                c2.sync()
+        for k in range(9):
+            print(f"[gpu] overlapped b32 step {k} on stream {k % 3}", flush=True)
+            parts[k % 3].run()
+            if k % 3 == 2:
+                for c in ctxs:
+                    c.sync()
                 for i, part in enumerate(parts):
                     got = part.output(1).download()
                     assert got.tobytes() == eager.tobytes(), f"stream {i} step {k} differs"
     finally:
         for part in parts:
             part.close()
-        c2.close()
+        for c in extra:
+            c.close()
 
 
 def llama_layers(lm, n_layers):
