@@ -233,3 +233,56 @@ def test_argmax_tie_rules(orc):
     v1001[0] = 9.0
     v1001[10] = 3.0
     assert orc.top1_reference(v1001)[0] == 9      # background class skipped, offset by one
+
+
+def _act_ref(v, act, alpha):
+    """float64 activation formulas, written from their definitions (relu.comp, relu6.comp,
+    leaky_relu.comp:17 max(alpha*x, x), sigmoid.comp, tanh.comp, SiLU x*sigmoid(x), GELU
+    0.5*x*erfc(-x/sqrt(2)))."""
+    from scipy.special import erfc
+    return {"none": v, "relu": np.maximum(v, 0.0), "relu6": np.clip(v, 0.0, 6.0),
+            "leaky": np.maximum(alpha * v, v), "sigmoid": 1.0 / (1.0 + np.exp(-v)),
+            "tanh": np.tanh(v), "silu": v / (1.0 + np.exp(-v)),
+            "gelu_erf": 0.5 * v * erfc(-v / np.sqrt(2.0))}[act]
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "relu6", "leaky", "sigmoid", "tanh", "silu",
+                                 "gelu_erf"])
+def test_gemv_nt_with_epilogue_vs_float64(orc, act):
+    """gemv_nt (the decode GEMV: y[n] = sum_k x[k] W[n][k]) with bias, residual and each
+    activation against float64 numpy."""
+    N, K = 300, 517
+    x, W = rnd(K), rnd(N, K, scale=0.1)
+    bias, res = rnd(N), rnd(N)
+    lin = W.astype(np.float64) @ x.astype(np.float64)
+    y = orc.run("gemv_nt", x, W, N, [N, K], bias=bias, residual=res, act=act, alpha=0.2)
+    assert_close(y, _act_ref(lin + bias + res, act, 0.2), 1e-5, 1e-5, f"gemv_nt {act}")
+    y0 = orc.run("gemv_nt", x, W, N, [N, K])
+    assert_close(y0, lin, 1e-5, 1e-5, "gemv_nt plain")
+
+
+@pytest.mark.parametrize("act", ["relu", "relu6", "gelu_erf"])
+def test_conv_epilogue_bias_per_channel_vs_float64(orc, act):
+    """The fused epilogue on a convolution: bias indexed by the output channel (last NHWC
+    dim), the residual in the output's layout, then the activation."""
+    n, ih, ic, oc = 2, 6, 8, 12
+    x, w = rnd(n, ih, ih, ic), rnd(3, 3, ic, oc, scale=0.3)
+    bias = rnd(oc)
+    lin = conv_nhwc_ref(x, w, (1, 1), (1, 1))
+    res = rnd(*lin.shape)
+    push = [n, ih, ih, ic, 3, 3, oc, ih, ih, 1, 1, 1, 1, lin.size]
+    y = orc.run("hlo_conv_nhwc_hwio", x, w, lin.size, push, bias=bias, residual=res, act=act)
+    assert_close(y, _act_ref(lin + bias + res, act, 0.0), 1e-5, 1e-5, f"conv epilogue {act}")
+
+
+def test_gather_rows_vs_numpy_take(orc):
+    """gather_rows: embed_table[ids] (run_llama_spirv.py:203), ids stored as int32 bits; an
+    id outside [0, rows) gives a zero row."""
+    rows, length = 50, 33
+    table = rnd(rows, length)
+    ids = np.array([3, 0, 49, 7, 3, -1, 50], np.int32)
+    y = orc.run("gather_rows", ids.view(np.float32), table, ids.size * length,
+                [ids.size, length, rows]).reshape(ids.size, length)
+    ok = (ids >= 0) & (ids < rows)
+    assert y[ok].tobytes() == np.take(table, ids[ok], axis=0).tobytes()
+    assert not y[~ok].any()
