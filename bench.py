@@ -6,17 +6,14 @@ graph, with TinyLlama-1.1B fp32 greedy decode tok/s an
 roofline fractions reported beside it.  Synthetic seeded inputs and random-init weights,
 generated on the device; inputs are resident in HBM before the timed region starts.
 
-Timed region: K steps of 32 images over `--streams` contexts (default three; one HIP stream,
-split-K workspace and hipGraph capture each, identical weights from the same seed).  With
-`--overlap steps` (default) whole b32 steps are dealt round-robin over the streams, so up to
-three independent batches are in flight at once; with `--overlap split` each step runs as concurrent
-sub-batches (two of 16).  Host wall clock around the K steps gives value and ms_per_step.  The
-concurrent chains fill the CUs that one chain's tile-count tails and per-tile prologue/epilogue
-phases leave idle.  The single-stream b32 graph replay is timed too and reported beside it.
-Profiled region: K b32 passes launched eagerly on one stream with a hipEvent pair around every
-kernel; those per-kernel durations give the roofline of the dominant kernel (the MFMA
-implicit-GEMM convolution), free of overlap between launches.  The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on
-a bounded sample of the same workload on this box's host cores.
+Timed region (`value`): K b32 steps, each one replay of a hipGraph capture of the whole
+forward on one HIP stream (one b32 chain), bracketed by stream synchronisation, host clock.
+Profiled region: K b32 passes launched eagerly on the same stream with a hipEvent pair around
+every kernel; those per-kernel durations give the roofline of the dominant kernel (the MFMA
+implicit-GEMM convolution).  Reported beside the headline, not as it: throughput with
+`--concurrency` independent b32 steps in flight on as many streams (extra.concurrent).
+The CPU baseline is the C oracle (restated reference loops, OpenMP) timed on bounded samples
+of the same workloads on this box's host cores, all cores and one thread.
 
 Prints ONE JSON line.  --gpus N > 1 exits with an explanation (single-GPU build).
 """
@@ -86,45 +83,6 @@ def measured_decode_traffic(n_prompt: int, n_new: int):
     return None
 
 
-def time_split_streams(ctx, m, steps: int, warmup: int, batch: int, streams: int):
-    """K steps of the b{batch} forward as `streams` concurrent sub-batches: one context (its
-    own HIP stream and split-K workspace) and one hipGraph per sub-batch, the same weights (same
-    seed), inputs the consecutive slices of m's input.  Returns (img/s, ms per step, top-1)."""
-    from spirv_inference_amd import Context
-    from spirv_inference_amd.models import Model
-    sub = batch // streams
-    x = m.input(0).download().reshape(batch, -1)
-    ctxs = [ctx] + [Context("any") for _ in range(streams - 1)]
-    parts = []
-    try:
-        for i, c in enumerate(ctxs):
-            part = Model(c, "resnet50_v1_5", sub, seed=2)
-            parts.append(part)
-            part.input(0).upload(x[i * sub:(i + 1) * sub])
-            part.use_graph(True)
-        for _ in range(max(warmup, 1)):
-            for part in parts:
-                part.run()
-        for c in ctxs:
-            c.sync()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            for part in parts:
-                part.run()
-        for c in ctxs:
-            c.sync()
-        elapsed = time.perf_counter() - t0
-        top1 = []
-        for part in parts:
-            top1 += [int(i) for i in np.argmax(part.output(1).download().reshape(sub, -1), axis=1)]
-        return batch * steps / elapsed, elapsed / steps * 1e3, top1
-    finally:
-        for part in parts:
-            part.close()
-        for c in ctxs[1:]:
-            c.close()
-
-
 def time_alternating_steps(ctx, m, steps: int, warmup: int, batch: int, streams: int):
     """K b{batch} steps dealt round-robin over `streams` contexts (one HIP stream and hipGraph
     each, same weights and input), so consecutive steps overlap.  Returns (img/s, ms/step, top-1)."""
@@ -159,8 +117,7 @@ def time_alternating_steps(ctx, m, steps: int, warmup: int, batch: int, streams:
             c.close()
 
 
-def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1,
-                 overlap: str = "split"):
+def bench_resnet(ctx, steps: int, warmup: int, batch: int, concurrency: int = 1):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
     flops, wbytes = m.work()
@@ -205,12 +162,15 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int, streams: int = 1,
         conv_ms_per_step=conv_ms / steps, conv_launches=conv_n,
         conv_avg_launch_ms=conv_ms / max(conv_n, 1), achieved_tflops=achieved,
         per_kernel_ms={k: v[0] / steps for k, v in sorted(rep.items())}, top1=top1,
-        weight_bytes=wbytes, streams=1, single_img_s=batch * steps / elapsed,
-        single_ms_per_step=elapsed / steps * 1e3, split_top1=None)
-    if streams > 1 and (overlap == "steps" or batch % streams == 0):
-        fn = time_split_streams if overlap == "split" else time_alternating_steps
-        img_s, ms, split_top1 = fn(ctx, m, steps, warmup, batch, streams)
-        res.update(img_s=img_s, ms_per_step=ms, streams=streams, split_top1=split_top1)
+        weight_bytes=wbytes, concurrent=None)
+    if concurrency > 1:
+        img_s, ms, top1_c = time_alternating_steps(ctx, m, steps, warmup, batch, concurrency)
+        res["concurrent"] = dict(streams=concurrency, img_s=round(img_s, 3),
+                                 ms_per_step=round(ms, 4), top1_identical=top1_c == top1,
+                                 region=f"K b{batch} steps dealt round-robin over {concurrency} "
+                                        "contexts (one HIP stream and hipGraph each), so up to "
+                                        f"{concurrency} independent b{batch} steps are in "
+                                        "flight; host clock")
     m.close()
     return res
 
@@ -278,25 +238,39 @@ def bench_decode(ctx, n_new: int, n_prompt: int):
                 engine=engine, graph_tok_s=1.0 / graph_s, graph_tokens_match=graph_gen == gen)
 
 
-def cpu_baseline_resnet(ctx, sample: int, gpu_top1):
-    """Oracle forward of the first `sample` images of the b32 batch (identical inputs and
-    weights: both depend only on (seed, tensor id, element index))."""
-    import oracle
+def cpu_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_model(ctx, arch: str, sample: int, seq_len: int = 0, gpu_top1=None):
+    """Oracle forward of the first `sample` inputs of a config's batch: inputs and weights
+    depend only on (seed, tensor id, element index), so a batch-`sample` graph holds exactly
+    those inputs of the full batch."""
     from oracle import walk
     from spirv_inference_amd.models import Model
-    m = Model(ctx, "resnet50_v1_5", sample, seed=2)
+    m = Model(ctx, arch, sample, seq_len, seed=2)
     host = walk.load_constants(m)
     t0 = time.perf_counter()
     out = walk.chained(m, host)
     t1 = time.perf_counter()
-    logits = out[m.ops()[-2].out].reshape(sample, -1)
-    cpu_top1 = [int(i) for i in np.argmax(logits, axis=1)]
+    res = dict(value=sample / (t1 - t0), seconds=t1 - t0, sample=sample)
+    if gpu_top1 is not None:
+        logits = out[m.ops()[-2].out].reshape(sample, -1)
+        top1 = [int(i) for i in np.argmax(logits, axis=1)]
+        res.update(top1=top1, top1_match=top1 == list(gpu_top1[:sample]))
     m.close()
-    return dict(value=sample / (t1 - t0), seconds=t1 - t0, top1=cpu_top1,
-                top1_match=cpu_top1 == list(gpu_top1[:sample]))
+    return res
 
 
 def cpu_baseline_decode(dec, n_steps: int):
+    """The oracle's KV-cache decode of n_steps tokens after the same prompt (the cache is
+    built untimed), on the decoder's own weights."""
     import oracle
     from spirv_inference_amd.models import TINYLLAMA
     lm = dec["lm"]
@@ -328,11 +302,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=32)
-    ap.add_argument("--streams", type=int, default=3,
-                    help="concurrent sub-batches (streams) a step is split into; 1 = one b32 chain")
-    ap.add_argument("--overlap", choices=("split", "steps"), default="steps",
-                    help="split: each step as concurrent sub-batches; steps: whole b32 steps "
-                         "dealt round-robin over the streams")
+    ap.add_argument("--concurrency", type=int, default=3,
+                    help="also time this many independent b32 steps in flight on as many "
+                         "streams (reported in extra.concurrent, not as the headline); 1 = skip")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--prompt-tokens", type=int, default=32)
     ap.add_argument("--cpu-sample", type=int, default=32, help="images for the CPU baseline")
@@ -353,15 +325,14 @@ def main() -> int:
     from spirv_inference_amd import Context
     ctx = Context("any")
     log(f"device {ctx.device_name}")
-    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.streams, args.overlap)
-    if rn["streams"] > 1:
-        how = ("b%d steps round-robin over" % args.batch if args.overlap == "steps"
-               else "sub-batches on")
-        log(f"resnet50 b{args.batch}, {how} {rn['streams']} concurrent streams: "
-            f"{rn['img_s']:.1f} img/s (single stream {rn['single_img_s']:.1f}); top-1 identical "
-            f"to the single-stream chain: {rn['split_top1'] == rn['top1']}")
-    log(f"resnet50 b{args.batch}: {rn['img_s']:.1f} img/s, {rn['ms_per_step']:.3f} ms/step "
-        f"(eager+events {rn['eager_ms_per_step']:.3f} ms), conv {rn['achieved_tflops']:.1f} TFLOP/s")
+    rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.concurrency)
+    log(f"resnet50 b{args.batch} (one chain): {rn['img_s']:.1f} img/s, "
+        f"{rn['ms_per_step']:.3f} ms/step (eager+events {rn['eager_ms_per_step']:.3f} ms), "
+        f"conv {rn['achieved_tflops']:.1f} TFLOP/s")
+    if rn["concurrent"]:
+        cc = rn["concurrent"]
+        log(f"resnet50 b{args.batch}, {cc['streams']} steps in flight on {cc['streams']} "
+            f"streams: {cc['img_s']:.1f} img/s (top-1 identical {cc['top1_identical']})")
     configs = {}
     if not args.no_configs:
         for arch, b, sl in (("mobilenet_v2", 1, 0), ("efficientnet_lite0", 8, 0),
@@ -377,20 +348,34 @@ def main() -> int:
             f"{dec['achieved_gbs']:.0f} GB/s; graph engine {dec['graph_tok_s']:.1f} tok/s "
             f"(tokens identical {dec['graph_tokens_match']})")
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    cpu = None
-    cpu_dec = None
+    cpu = cpu1 = cpu_dec = cpu_dec1 = None
+    cpu_cfg = {}
     if not args.no_cpu_baseline:
         import oracle
         oracle.set_threads(cores)
-        cpu = cpu_baseline_resnet(ctx, args.cpu_sample, rn["top1"])
+        cpu = cpu_baseline_model(ctx, "resnet50_v1_5", args.cpu_sample, gpu_top1=rn["top1"])
         log(f"cpu oracle resnet: {cpu['value']:.3f} img/s on {cores} threads "
             f"(top1 match {cpu['top1_match']})")
+        for arch, sample, sl in (("mobilenet_v2", 1, 0), ("efficientnet_lite0", 8, 0),
+                                 ("bert_base", 1, 128)):
+            r = cpu_baseline_model(ctx, arch, sample, sl)
+            cpu_cfg[arch] = {"ms_per_input": round(r["seconds"] / sample * 1e3, 2),
+                             "sample": f"{sample} of the config's inputs, {cores} threads"}
+            log(f"cpu oracle {arch}: {r['seconds'] / sample * 1e3:.1f} ms per input")
         if dec is not None:
             cpu_dec = cpu_baseline_decode(dec, args.cpu_decode_steps)
             log(f"cpu oracle decode: {cpu_dec['value']:.3f} tok/s "
                 f"(tokens match {cpu_dec['tokens_match']})")
+        oracle.set_threads(1)
+        cpu1 = cpu_baseline_model(ctx, "resnet50_v1_5", 1, gpu_top1=rn["top1"])
+        log(f"cpu oracle resnet, 1 thread: {cpu1['value']:.3f} img/s")
+        if dec is not None:
+            cpu_dec1 = cpu_baseline_decode(dec, 3)
+            log(f"cpu oracle decode, 1 thread: {cpu_dec1['value']:.3f} tok/s")
+        oracle.set_threads(cores)
 
     traffic = measured_conv_traffic(args.batch)
+    host_cpu = cpu_model()
     line = {
         "metric": METRIC,
         "value": round(rn["img_s"], 3),
@@ -408,12 +393,10 @@ def main() -> int:
             "workload": f"ResNet-50 v1.5 fp32 inference, batch {args.batch}, NHWC "
                         f"{args.batch}x224x224x3 N(0,1), HLO path (hlo_conv_nhwc_hwio, "
                         "reduce_window max-pool, mean pool, dot 2048->1000, softmax), "
-                        "He-normal weights with folded BN",
+                        "He-normal weights (the last 1x1 conv of each bottleneck at 0.2x He, "
+                        "its folded-BN gamma), folded BN as a bias N(0,0.01); one b32 chain",
             "global_batch": args.batch,
-            "streams": rn["streams"],
-            "overlap": args.overlap if rn["streams"] > 1 else None,
-            "batch_per_launch": (args.batch // rn["streams"]
-                                 if rn["streams"] > 1 and args.overlap == "split" else args.batch),
+            "streams": 1,
             "flops_per_img": rn["flops_per_img"],
             "seed": 2,
         },
@@ -434,24 +417,22 @@ def main() -> int:
         },
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["value"], 4), "unit": "img/s", "cores": cores, "kind": "port",
+            "cpu": host_cpu,
             "sample": f"C oracle (reference kernel loops, OpenMP) forward of images 0..{args.cpu_sample - 1} "
                       f"of the same b{args.batch} workload, {cpu['seconds']:.2f} s; "
                       f"top-1 identical to the GPU's: {cpu['top1_match']}",
+            "one_thread": None if cpu1 is None else {
+                "value": round(cpu1["value"], 4), "unit": "img/s", "cores": 1,
+                "sample": f"image 0, {cpu1['seconds']:.2f} s; top-1 identical: "
+                          f"{cpu1['top1_match']}"},
+            "configs": cpu_cfg,
         },
         "extra": {
-            "timed_region": ((f"K b{args.batch} steps dealt round-robin over {rn['streams']} "
-                              f"HIP streams (one hipGraph each, {rn['streams']} steps in flight), host clock"
-                              if args.overlap == "steps" else
-                              f"K steps of {args.batch} images as {rn['streams']} concurrent "
-                              "sub-batches (one HIP stream + hipGraph each), host clock")
-                             if rn["streams"] > 1 else
-                             "hipGraph replay of the whole step, K times, host clock"),
+            "timed_region": "hipGraph replay of the whole b32 step on one HIP stream, K times, "
+                            "host clock",
             "profiled_region": f"K b{args.batch} steps launched eagerly on one stream with a "
                                "hipEvent pair per kernel (roofline source)",
-            "single_stream_img_s": round(rn["single_img_s"], 3),
-            "single_stream_ms_per_step": round(rn["single_ms_per_step"], 4),
-            "split_top1_identical": (None if rn["split_top1"] is None
-                                     else rn["split_top1"] == rn["top1"]),
+            "concurrent": rn["concurrent"],
             "eager_ms_per_step": round(rn["eager_ms_per_step"], 4),
             "kernel_ms_per_step": round(rn["kernel_ms_per_step"], 4),
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},
@@ -462,9 +443,9 @@ def main() -> int:
     if dec is not None:
         line["decode"] = {
             "workload": "TinyLlama-1.1B-shape fp32 greedy decode, batch 1, 22 layers, hidden 2048, "
-                        "32q/4kv heads, SwiGLU 5632, vocab 32000, N(0,0.02) weights, "
-                        f"{args.prompt_tokens} seeded prompt ids, {args.decode_tokens} new tokens "
-                        "(KV cache; timed: one decode call of the default engine)",
+                        "32q/4kv heads, SwiGLU 5632, vocab 32000, N(0,0.02) weights, RMSNorm "
+                        f"weights 1, {args.prompt_tokens} seeded prompt ids, {args.decode_tokens} "
+                        "new tokens (KV cache; timed: one decode call of the default engine)",
             "value": round(dec["tok_s"], 3), "unit": "tok/s",
             "ms_per_token": round(dec["ms_per_token"], 4),
             "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbs"], 1),
@@ -482,10 +463,13 @@ def main() -> int:
             "graph_engine_tokens_identical": dec["graph_tokens_match"],
             "cpu_baseline": None if cpu_dec is None else {
                 "value": round(cpu_dec["value"], 4), "unit": "tok/s", "cores": cores,
-                "kind": "port",
+                "kind": "port", "cpu": host_cpu,
                 "sample": f"C oracle KV-cache decode of {args.cpu_decode_steps} tokens after the "
                           f"same prompt, {cpu_dec['seconds']:.2f} s; tokens identical to the "
-                          f"GPU's: {cpu_dec['tokens_match']}"},
+                          f"GPU's: {cpu_dec['tokens_match']}",
+                "one_thread": None if cpu_dec1 is None else {
+                    "value": round(cpu_dec1["value"], 4), "unit": "tok/s", "cores": 1,
+                    "sample": f"3 tokens, {cpu_dec1['seconds']:.2f} s"}},
         }
         dec["lm"].close()
     if args.copy_calibration_mb > 0:

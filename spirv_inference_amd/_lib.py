@@ -124,6 +124,14 @@ SIGNATURES = [
     ("shp_llama_weight_bytes", C.c_int, [C.c_void_p, C.POINTER(C.c_double)]),
 ]
 
+# Internal hooks for tests and experiments, exported by the library but not declared in
+# include/spirv_hip.h: per-context planner overrides and split-K workspace control.
+INTERNAL = [
+    ("shp_tune", C.c_int, [C.c_void_p, C.c_char_p, C.c_int]),
+    ("shp_reserve_workspace", C.c_int, [C.c_void_p, C.c_uint64]),
+    ("shp_workspace_info", C.c_int, [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
+]
+
 _LIB = None
 
 
@@ -136,7 +144,7 @@ def lib() -> C.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
                 "g.build()'` (there is no CPU fallback)")
         h = C.CDLL(str(LIB_PATH))
-        for name, res, args in SIGNATURES:
+        for name, res, args in SIGNATURES + INTERNAL:
             fn = getattr(h, name, None)
             if fn is None:  # completeness is enforced by tests/test_abi.py
                 continue

@@ -25,6 +25,13 @@ int fail(int code, const std::string& msg);
                                                 hipGetErrorString(e__));             \
     } while (0)
 
+// Planner overrides of the dense kernels, held per context (all 0 = automatic choice):
+// tile 1: 128x128, 2: 128x64, 3: 64x64; bk 16 or 32; splits: split-K count; dma 0 automatic,
+// -1 never, 1: 128x128, 2: 128x64 pipelined kernel; pg: register prefetch depth 1 or 2.
+struct GemmTune {
+    int tile = 0, bk = 0, splits = 0, dma = 0, pg = 0;
+};
+
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.
 struct Launch {
     hipStream_t stream;
@@ -37,6 +44,7 @@ struct Launch {
     const shp_epilogue* epi;  // never null inside launchers (zero epilogue if absent)
     float* workspace;         // context-owned scratch (split-K partials), may be null
     size_t workspace_bytes;
+    const GemmTune* tune;     // the context's planner overrides (null: none)
 };
 
 using LaunchFn = int (*)(const Launch&);
@@ -67,7 +75,12 @@ const KernelEntry* find_kernel(const char* name);
 // Launch a registered kernel on a stream (used by the graph runtime and the models).
 int launch_kernel(hipStream_t stream, const char* name, const void* in0, const void* in1,
                   void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
-                  const shp_epilogue* epi, float* workspace, size_t workspace_bytes);
+                  const shp_epilogue* epi, float* workspace, size_t workspace_bytes,
+                  const GemmTune* tune);
+
+// Split-K workspace a dense kernel would ask for with this push vector (0 if none).
+size_t gemm_workspace_for_kernel(const char* name, const int32_t* push, size_t n_push,
+                                 const GemmTune* tune);
 
 // Counter-based RNG fill (kernels_elementwise.hip).
 int fill_random(hipStream_t stream, float* p, uint64_t n, uint64_t seed, uint64_t tensor_id,

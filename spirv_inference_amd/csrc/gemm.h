@@ -55,12 +55,14 @@ struct GemmParams {
 // launch leaves them zero again.  The partials follow.
 constexpr size_t kSplitCounterBytes = 65536;
 
-// Launch C = epilogue(A*B) for the problem; picks tile shape and split-K.
-// `workspace`/`workspace_bytes` provide the split-K partials (may be null: no split).
+// Launch C = epilogue(A*B) for the problem; picks tile shape and split-K (`tune` may force
+// parts of that choice, or be null).  `workspace`/`workspace_bytes` provide the split-K
+// partials (may be null: no split).
 int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
-                float* workspace, size_t workspace_bytes);
+                float* workspace, size_t workspace_bytes, const GemmTune* tune);
 
 // Workspace the launcher would like for this problem (0 if it will not split K).
-size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode);
+size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode,
+                            const GemmTune* tune);
 
 }  // namespace shp

@@ -944,13 +944,6 @@ struct TileCfg {
     int pg;    // gemm_mfma_kernel global prefetch depth (0 or 1: one tile, 2: two tiles)
 };
 
-// Internal tuning overrides (0 = automatic); set through shp_tune() by experiments only.
-int g_force_tile = 0;    // 1: 128x128, 2: 128x64, 3: 64x64
-int g_force_bk = 0;      // 16 or 32
-int g_force_splits = 0;  // split-K count
-int g_force_dma = 0;     // pipelined DMA kernel: 0 automatic, -1 never, 1: 128x128, 2: 128x64
-int g_force_pg = 0;      // gemm_mfma_kernel prefetch depth: 0 automatic, 1 or 2
-
 // The pipelined kernel takes row-contiguous operands whose 16-byte chunks are aligned:
 // A rows (or an NHWC input whose channel count is a multiple of its K tile) and [K][N] B.
 bool dma_eligible(const GemmParams& p, int am, int bm, int cm) {
@@ -1096,25 +1089,26 @@ double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps
     return cost;
 }
 
-Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv_a) {
+Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv_a,
+               const shp::GemmTune& tn) {
     static const int kTiles[5][2] = {{128, 128}, {128, 64}, {64, 64}, {128, 128}, {128, 64}};
     static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 12, 16};
-    if (dma_ok && conv_a && g_force_dma == 0 && !g_force_splits && dma_preferred(p, nbatch))
+    if (dma_ok && conv_a && tn.dma == 0 && !tn.splits && dma_preferred(p, nbatch))
         return Plan{{128, 64, 16, true}, 1, ((p.K + 31) / 32) * 32};
     Plan best{{128, 128, 32, false}, 1, 0};
     double best_cost = 1e30;
     for (int ti = 0; ti < 5; ++ti) {
         const bool dma = ti >= 3;
-        if (dma && (!dma_ok || g_force_dma <= 0 || g_force_dma != ti - 2)) continue;
-        if (!dma && dma_ok && g_force_dma > 0) continue;
-        if (!dma && g_force_tile && g_force_tile != ti + 1) continue;
+        if (dma && (!dma_ok || tn.dma <= 0 || tn.dma != ti - 2)) continue;
+        if (!dma && dma_ok && tn.dma > 0) continue;
+        if (!dma && tn.tile && tn.tile != ti + 1) continue;
         for (int bk : {32, 16}) {
             if (dma && bk != 16) continue;
             if (!dma && bk == 16 && !hot) continue;
-            if (!dma && g_force_bk && g_force_bk != bk) continue;
+            if (!dma && tn.bk && tn.bk != bk) continue;
             TileCfg t{kTiles[ti][0], kTiles[ti][1], bk, dma};
             for (int s : kSplits) {
-                if (g_force_splits && g_force_splits != s) continue;
+                if (tn.splits && tn.splits != s) continue;
                 int kps = (p.K + s - 1) / s;
                 kps = ((kps + 31) / 32) * 32;  // a multiple of both K tiles
                 if (kps <= 0) kps = 32;
@@ -1137,15 +1131,19 @@ Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv
 
 namespace shp {
 
-size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode) {
+size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode,
+                            const GemmTune* tune) {
+    static const GemmTune kAuto;
     int nbatch = p.batch_outer * p.batch_inner;
     Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
-                        dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4);
+                        dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4,
+                        tune ? *tune : kAuto);
     if (pl.splits <= 1) return 0;
     return kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
 }
 
-size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
+size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
+                                 const GemmTune* tune) {
     GemmParams p;
     memset(&p, 0, sizeof(p));
     p.batch_outer = p.batch_inner = 1;
@@ -1174,12 +1172,14 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n) {
     }
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) return 0;
     // the largest of the hot and generic plans, so either launch finds its partials
-    return std::max(gemm_workspace_bytes(p, am, bm, C_STRIDED),
-                    gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED));
+    return std::max(gemm_workspace_bytes(p, am, bm, C_STRIDED, tune),
+                    gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED, tune));
 }
 
 int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
-                float* workspace, size_t workspace_bytes) {
+                float* workspace, size_t workspace_bytes, const GemmTune* tune) {
+    static const GemmTune kAuto;
+    const GemmTune& tn = tune ? *tune : kAuto;
     if (p.M <= 0 || p.N <= 0 || p.K < 0)
         return fail(SHP_ERR_SHAPE, "gemm: M, N must be > 0 and K >= 0");
     int nbatch = p.batch_outer * p.batch_inner;
@@ -1192,7 +1192,7 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     const bool fix_ok = cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 && (p.N & 3) == 0 &&
                         (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
                         (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual));
-    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4);
+    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn);
     size_t need = pl.splits > 1
                       ? kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float)
                       : 0;
@@ -1212,7 +1212,7 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     if (!t.dma && t.bm == 64 && t.bn == 64 && t.bk == 32 && pl.splits > 1 &&
         amode == A_CONV_NHWC4 && combo_is_hot(amode, bmode, cmode))
         t.pg = 2;
-    if (g_force_pg) t.pg = g_force_pg;
+    if (tn.pg) t.pg = tn.pg;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
     if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
     // in-kernel split-K fixup where the tile counters fit and few splits share a tile (the last
@@ -1240,18 +1240,6 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
 }
 
 }  // namespace shp
-
-// Internal tuning hook for experiments (not part of include/spirv_hip.h).
-extern "C" int shp_tune(const char* key, int value) {
-    std::string k = key ? key : "";
-    if (k == "gemm_tile") g_force_tile = value;
-    else if (k == "gemm_bk") g_force_bk = value;
-    else if (k == "gemm_splits") g_force_splits = value;
-    else if (k == "gemm_dma") g_force_dma = value;
-    else if (k == "gemm_pg") g_force_pg = value;
-    else return SHP_ERR_INVALID;
-    return SHP_OK;
-}
 
 namespace {
 
@@ -1297,7 +1285,8 @@ int launch_hlo_conv(const shp::Launch& l) {
     p.alpha = l.epi->alpha;
     int am = (p.cic % 4 == 0 && al16(p.a)) ? shp::A_CONV_NHWC4 : shp::A_CONV_NHWC;
     int bm = (p.N % 4 == 0 && al16(p.b)) ? shp::B_NVEC : shp::B_STRIDED;
-    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes,
+                            l.tune);
 }
 
 // conv2d (NCHW, weights OIHW followed by the bias tail):
@@ -1333,10 +1322,10 @@ int conv2d_common(const shp::Launch& l, bool nhwc) {
     if (nhwc) {
         int am = (p.cic % 4 == 0 && al16(p.a)) ? shp::A_CONV_NHWC4 : shp::A_CONV_NHWC;
         return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace,
-                                l.workspace_bytes);
+                                l.workspace_bytes, l.tune);
     }
     return shp::gemm_launch(l.stream, p, shp::A_CONV_NCHW, bm, shp::C_NCHW, l.workspace,
-                            l.workspace_bytes);
+                            l.workspace_bytes, l.tune);
 }
 
 int launch_conv2d(const shp::Launch& l) { return conv2d_common(l, false); }
@@ -1379,7 +1368,8 @@ int launch_fully_connected(const shp::Launch& l) {
     p.alpha = l.epi->alpha;
     int am = (K % 4 == 0 && al16(p.a)) ? shp::A_KVEC : shp::A_STRIDED;
     int bm = (K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
-    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes,
+                            l.tune);
 }
 
 // Pick vector modes for a strided batched product when the layout allows them.
@@ -1421,7 +1411,8 @@ int launch_dot_batched(const shp::Launch& l) {
     dot_epilogue(p, l);
     int am, bm;
     dot_modes(p, am, bm);
-    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes,
+                            l.tune);
 }
 
 // hlo_dot_rank2: push {m, k, n, total}
@@ -1441,7 +1432,8 @@ int launch_dot_rank2(const shp::Launch& l) {
     dot_epilogue(p, l);
     int am, bm;
     dot_modes(p, am, bm);
-    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes,
+                            l.tune);
 }
 
 // dot_general_strided (native): any dot_general with one contracting dim, read in place.
@@ -1466,7 +1458,8 @@ int launch_dot_general(const shp::Launch& l) {
     dot_epilogue(p, l);
     int am, bm;
     dot_modes(p, am, bm);
-    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes);
+    return shp::gemm_launch(l.stream, p, am, bm, shp::C_STRIDED, l.workspace, l.workspace_bytes,
+                            l.tune);
 }
 
 }  // namespace

@@ -65,7 +65,4 @@ int build_mobilenet_v2(Model& m, int batch);
 int build_efficientnet_lite0(Model& m, int batch);
 int build_bert_base(Model& m, int batch, int seq);
 
-// Split-K workspace a dense kernel would ask for with this push vector (0 if none).
-size_t gemm_workspace_for_kernel(const char* name, const int32_t* push, size_t n_push);
-
 }  // namespace shp

@@ -91,7 +91,8 @@ int Model::op(const char* kernel, int in0, int in1, int out, std::vector<int32_t
     o.alpha = alpha;
     o.out_elems = tensors[out].elems;
     workspace_need = std::max(workspace_need,
-                              gemm_workspace_for_kernel(kernel, o.push.data(), o.push.size()));
+                              gemm_workspace_for_kernel(kernel, o.push.data(), o.push.size(),
+                                                        &ctx->tune));
     ops.push_back(std::move(o));
     return (int)ops.size() - 1;
 }

@@ -59,11 +59,10 @@ const KernelEntry* find_kernel(const char* name) {
     return nullptr;
 }
 
-size_t gemm_workspace_for_kernel(const char* name, const int32_t* push, size_t n_push);
-
 int launch_kernel(hipStream_t stream, const char* name, const void* in0, const void* in1,
                   void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
-                  const shp_epilogue* epi, float* workspace, size_t workspace_bytes) {
+                  const shp_epilogue* epi, float* workspace, size_t workspace_bytes,
+                  const GemmTune* tune) {
     const KernelEntry* e = find_kernel(name);
     if (!e) return fail(SHP_ERR_UNKNOWN_KERNEL, std::string("unknown kernel '") +
                                                     (name ? name : "(null)") + "'");
@@ -77,7 +76,7 @@ int launch_kernel(hipStream_t stream, const char* name, const void* in0, const v
         return fail(SHP_ERR_UNSUPPORTED, std::string(name) + ": kernel has no fused epilogue");
     if (out_elems > 0 && !out) return fail(SHP_ERR_INVALID, std::string(name) + ": null output");
     Launch l{stream, in0, in1, out, push, n_push, out_elems, epi ? epi : &kNone, workspace,
-             workspace_bytes};
+             workspace_bytes, tune};
     return e->fn(l);
 }
 
@@ -88,18 +87,18 @@ Ctx::~Ctx() {
         (void)hipEventDestroy(t.b);
     }
     if (workspace) (void)hipFree(workspace);
+    for (float* w : retired) (void)hipFree(w);
     if (own_stream) (void)hipStreamDestroy(own_stream);
 }
 
 int Ctx::ensure_workspace(size_t bytes) {
     if (bytes <= workspace_bytes) return SHP_OK;
-    if (workspace) {
-        SHP_HIP_CHECK(hipStreamSynchronize(stream));
-        SHP_HIP_CHECK(hipFree(workspace));
-        workspace = nullptr;
-        workspace_bytes = 0;
-    }
-    SHP_HIP_CHECK(hipMalloc((void**)&workspace, bytes));
+    float* grown = nullptr;
+    SHP_HIP_CHECK(hipMalloc((void**)&grown, bytes));
+    // The old buffer may be baked into a captured hipGraph (a model's or the caller's):
+    // keep it alive until the context goes away.
+    if (workspace) retired.push_back(workspace);
+    workspace = grown;
     workspace_bytes = bytes;
     // the split-K tile counters at its start must begin at zero (launches keep them zero)
     SHP_HIP_CHECK(hipMemset(workspace, 0, std::min(bytes, kSplitCounterBytes)));
@@ -113,7 +112,7 @@ int Ctx::launch(const char* name, const void* in0, const void* in1, void* out,
     // launch that asks for more, except while the stream is being captured into a graph
     // (no allocation there; such a launch runs without splitting K).  Model graphs size it
     // before they capture.
-    const size_t need = name ? gemm_workspace_for_kernel(name, push, n_push) : 0;
+    const size_t need = name ? gemm_workspace_for_kernel(name, push, n_push, &tune) : 0;
     if (need > workspace_bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         SHP_HIP_CHECK(hipStreamIsCapturing(stream, &cs));
@@ -135,7 +134,7 @@ int Ctx::launch(const char* name, const void* in0, const void* in1, void* out,
         SHP_HIP_CHECK(hipEventRecord(t->a, stream));
     }
     int rc = launch_kernel(stream, name, in0, in1, out, push, n_push, out_elems, epi, workspace,
-                           workspace_bytes);
+                           workspace_bytes, &tune);
     if (t) {
         if (rc) {
             --timer_used;
@@ -274,11 +273,35 @@ int shp_sync(shp_ctx* ctx) {
     return SHP_OK;
 }
 
-// Internal tuning hook for experiments (not part of include/spirv_hip.h): grow the context's
-// split-K workspace so forced split counts are not clamped by it.
+// Internal hooks for tests and experiments (not part of include/spirv_hip.h).
+// Grow the context's split-K workspace so forced split counts are not clamped by it.
 int shp_reserve_workspace(shp_ctx* ctx, uint64_t bytes) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_reserve_workspace: null ctx");
     return reinterpret_cast<Ctx*>(ctx)->ensure_workspace((size_t)bytes);
+}
+
+// Current split-K workspace of the context (its address and size), for lifetime checks.
+int shp_workspace_info(shp_ctx* ctx, void** dptr, uint64_t* bytes) {
+    if (!ctx || !dptr || !bytes) return fail(SHP_ERR_INVALID, "shp_workspace_info: null argument");
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    *dptr = c->workspace;
+    *bytes = c->workspace_bytes;
+    return SHP_OK;
+}
+
+// Force parts of the dense-kernel planner's choice for launches on this context only
+// (0 restores the automatic choice): gemm_tile, gemm_bk, gemm_splits, gemm_dma, gemm_pg.
+int shp_tune(shp_ctx* ctx, const char* key, int value) {
+    if (!ctx) return fail(SHP_ERR_INVALID, "shp_tune: null ctx");
+    shp::GemmTune& t = reinterpret_cast<Ctx*>(ctx)->tune;
+    std::string k = key ? key : "";
+    if (k == "gemm_tile") t.tile = value;
+    else if (k == "gemm_bk") t.bk = value;
+    else if (k == "gemm_splits") t.splits = value;
+    else if (k == "gemm_dma") t.dma = value;
+    else if (k == "gemm_pg") t.pg = value;
+    else return fail(SHP_ERR_INVALID, "shp_tune: unknown key '" + k + "'");
+    return SHP_OK;
 }
 
 int shp_fill_random(shp_ctx* ctx, float* dptr, uint64_t n, uint64_t seed, uint64_t tensor_id,

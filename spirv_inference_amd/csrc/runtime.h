@@ -16,8 +16,13 @@ struct Ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     shp_run_info info{};
+    // Split-K scratch of eager launches.  A graph captured from such a launch keeps the
+    // pointer it saw, so a buffer outgrown later is retired (kept until the context is
+    // destroyed) instead of freed.
     float* workspace = nullptr;
     size_t workspace_bytes = 0;
+    std::vector<float*> retired;
+    GemmTune tune;  // planner overrides of this context's dense launches (shp_tune)
 
     struct Timer {
         hipEvent_t a, b;

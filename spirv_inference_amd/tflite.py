@@ -613,6 +613,28 @@ class TfliteExecutor:
                 self.consts[t.index] = np.frombuffer(data, dtype="<i4").copy()
         self.packed: Dict[Tuple[int, int], object] = {}
         self.op_log: List[dict] = []
+        self._check_aliases()
+
+    def _check_aliases(self) -> None:
+        """The view ops' rules (scheduler.rs:230-249), checked before anything runs: Cast
+        only Float32 -> Float32, and the element count must not change (a view larger than
+        its source would read past that allocation)."""
+        for op in self.model.operators:
+            if op.builtin not in _ALIASES:
+                continue
+            if not op.inputs or op.inputs[0] < 0 or len(op.outputs) != 1:
+                raise ValueError(f"operator {op.index} {op.builtin} needs one data input and "
+                                 "one output")
+            src, dst = op.inputs[0], op.outputs[0]
+            if op.builtin == "CAST":
+                tin = self.model.tensors[src].tensor_type
+                tout = self.model.tensors[dst].tensor_type
+                if tin != "Float32" or tout != "Float32":
+                    raise ValueError(f"operator {op.index} Cast only supports Float32->Float32, "
+                                     f"got {tin}->{tout}")
+            if self._elems(src) != self._elems(dst):
+                raise ValueError(f"operator {op.index} {op.builtin} element count changed from "
+                                 f"{self._elems(src)} to {self._elems(dst)}")
 
     # -- helpers
     def _shape(self, idx: int) -> List[int]:
@@ -622,7 +644,12 @@ class TfliteExecutor:
         return int(np.prod(self._shape(idx))) if self._shape(idx) else 1
 
     def _alloc(self, idx: int):
-        t = self.ctx.empty(max(1, self._elems(idx)))
+        """The device buffer of tensor idx, allocated on first use and kept across runs."""
+        n = max(1, self._elems(idx))
+        t = self.dev.get(idx)
+        if t is not None and t.n == n:
+            return t
+        t = self.ctx.empty(n)
         self.owned.append(t)
         self.dev[idx] = t
         return t
@@ -669,10 +696,11 @@ class TfliteExecutor:
         v = np.ascontiguousarray(values, np.float32).reshape(-1)
         if v.size != self._elems(idx):
             raise ValueError(f"input has {v.size} values, tensor {idx} holds {self._elems(idx)}")
-        t = self.dev.get(idx) or self._alloc(idx)
+        t = self._alloc(idx)
         t.upload(v)
 
     def run(self) -> None:
+        self.op_log = []  # the dispatches of this run
         for oi in self.order:
             op = self.model.operators[oi]
             self.op_log.append({"index": op.index, "op": op.builtin,

@@ -303,10 +303,10 @@ def test_hlo_conv_full_batch(ctx, orc, ih, ic, k, oc, s):
 
 
 # ---- the pipelined GEMM kernel (operand tiles DMA'd straight into LDS) --------------------
-def _tune(key, value):
-    """Internal planner override of the library (shp_tune, not part of the C ABI header)."""
+def _tune(ctx, key, value):
+    """Planner override of one context (shp_tune, internal: not in the C ABI header)."""
     from spirv_inference_amd._lib import lib
-    assert lib().shp_tune(key.encode(), int(value)) == 0
+    assert lib().shp_tune(ctx.handle, key.encode(), int(value)) == 0
 
 
 @pytest.fixture
@@ -332,13 +332,13 @@ def test_hlo_conv_dma_pipeline(ctx, orc, gemm_workspace, tile, n, ih, ic, k, oc,
     b, res = rnd(oc, scale=0.01), rnd(n * oh * oh * oc)
     push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
     try:
-        _tune("gemm_dma", tile)
-        _tune("gemm_splits", splits)
+        _tune(ctx, "gemm_dma", tile)
+        _tune(ctx, "gemm_splits", splits)
         y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res,
                 act="relu")
     finally:
-        _tune("gemm_dma", 0)
-        _tune("gemm_splits", 0)
+        _tune(ctx, "gemm_dma", 0)
+        _tune(ctx, "gemm_splits", 0)
     r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res, act="relu")
     assert_close(y, r, 1e-4, 1e-4, f"dma conv {push[:13]} splits {splits}")
 
@@ -350,14 +350,14 @@ def test_dot_dma_pipeline(ctx, orc, tile, bt, m, k, n):
     a, b = rnd(bt, m, k), rnd(bt, k, n, scale=0.1)
     bias = rnd(n)
     try:
-        _tune("gemm_dma", tile)
+        _tune(ctx, "gemm_dma", tile)
         if bt == 1:
             y = hip(ctx, "hlo_dot_rank2", a[0], b[0], m * n, [m, k, n, m * n], bias=bias,
                     act="gelu_erf")
         else:
             y = hip(ctx, "hlo_dot_batched", a, b, bt * m * n, [bt, m, k, n, bt * m * n])
     finally:
-        _tune("gemm_dma", 0)
+        _tune(ctx, "gemm_dma", 0)
     if bt == 1:
         r = orc.run("hlo_dot_rank2", a[0], b[0], m * n, [m, k, n, m * n], bias=bias,
                     act="gelu_erf")
@@ -377,12 +377,12 @@ def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk, pg):
     cases = [((2, 9, 32, 3, 20, 1), 0), ((3, 8, 64, 1, 72, 1), 0), ((2, 6, 16, 1, 24, 1), 0),
              ((2, 7, 128, 3, 64, 1), 3)]
     try:
-        _tune("gemm_dma", -1)
-        _tune("gemm_tile", tile)
-        _tune("gemm_bk", bk)
-        _tune("gemm_pg", pg)
+        _tune(ctx, "gemm_dma", -1)
+        _tune(ctx, "gemm_tile", tile)
+        _tune(ctx, "gemm_bk", bk)
+        _tune(ctx, "gemm_pg", pg)
         for (n, ih, ic, k, oc, s), splits in cases:
-            _tune("gemm_splits", splits)
+            _tune(ctx, "gemm_splits", splits)
             pad = (k - 1) // 2
             oh = (ih + 2 * pad - k) // s + 1
             x = rnd(n, ih, ih, ic)
@@ -392,13 +392,13 @@ def test_gemm_tile_variants(ctx, orc, gemm_workspace, tile, bk, pg):
             y, r = both(ctx, orc, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b,
                         residual=res, act="relu")
             assert_close(y, r, 1e-4, 1e-4, f"conv {push[:13]} splits {splits}")
-        _tune("gemm_splits", 0)
+        _tune(ctx, "gemm_splits", 0)
         a, bm = rnd(1, 70, 100), rnd(1, 100, 36, scale=0.1)
         y, r = both(ctx, orc, "hlo_dot_batched", a, bm, 70 * 36, [1, 70, 100, 36, 70 * 36])
         assert_close(y, r, 1e-4, 1e-4, "dot 70x100x36")
     finally:
         for key in ("gemm_dma", "gemm_tile", "gemm_bk", "gemm_splits", "gemm_pg"):
-            _tune(key, 0)
+            _tune(ctx, key, 0)
 
 
 @pytest.mark.parametrize("splits", [2, 3, 6])
@@ -414,7 +414,7 @@ def test_splitk_in_kernel_fixup(ctx, orc, gemm_workspace, splits):
     push = [n, ih, ih, ic, 3, 3, oc, ih, ih, 1, 1, 1, 1, n * ih * ih * oc]
     r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res, act="relu")
     try:
-        _tune("gemm_splits", splits)
+        _tune(ctx, "gemm_splits", splits)
         for rep in range(3):
             y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, bias=b, residual=res,
                     act="relu")
@@ -426,7 +426,7 @@ def test_splitk_in_kernel_fixup(ctx, orc, gemm_workspace, splits):
             assert_close(y, orc.run("hlo_dot_batched", a, bm, bt * m * nn, q), 1e-4, 1e-4,
                          f"split-K dot {bt}x{m}x768x{nn}")
     finally:
-        _tune("gemm_splits", 0)
+        _tune(ctx, "gemm_splits", 0)
 
 
 def test_hlo_conv_dma_by_planner(ctx, orc):

@@ -169,3 +169,29 @@ def test_default_input_and_top1():
     h[0], h[7] = 9.0, 5.0
     t = T.top1(h)
     assert (t["model_class"], t["class"]) == (7, 6)
+
+
+def _alias_model(builtin, in_shape, out_shape, in_type=0, out_type=0):
+    w = T.TfliteWriter("alias check")
+    i = w.tensor("input", in_shape, ttype=in_type)
+    o = w.tensor("output", out_shape, ttype=out_type)
+    w.inputs, w.outputs = [i], [o]
+    w.op(builtin, [i], [o])
+    return T.parse_model(w.finish(), "alias.tflite")
+
+
+@pytest.mark.parametrize("builtin", ["RESHAPE", "SQUEEZE", "EXPAND_DIMS", "CAST"])
+def test_view_ops_reject_element_count_change(builtin):
+    """scheduler.rs:241-249: a view op may not change the element count.  The executor checks
+    it when it is built, before any device call (no context is touched here)."""
+    m = _alias_model(builtin, [1, 8], [1, 9])
+    with pytest.raises(ValueError, match="element count changed from 8 to 9"):
+        T.TfliteExecutor(None, m)
+    T.TfliteExecutor(None, _alias_model(builtin, [1, 8], [2, 4]))  # same count: accepted
+
+
+def test_cast_only_float32_to_float32():
+    """scheduler.rs:230-240: Cast must be Float32 -> Float32."""
+    m = _alias_model("CAST", [1, 8], [1, 8], in_type=2)  # Int32 -> Float32
+    with pytest.raises(ValueError, match="Cast only supports Float32->Float32, got Int32->Float32"):
+        T.TfliteExecutor(None, m)

@@ -132,6 +132,23 @@ def test_small_cnn_graph(ctx):
     assert kernels == ["conv2d_nhwc", "depthwise_conv2d_nhwc", "conv2d_nhwc", "add",
                        "hlo_reduce_window_rank4", "hlo_concatenate_into", "hlo_concatenate_into",
                        "global_avg_pool_nhwc", "fully_connected", "softmax1000"]
+    # one executor over several inputs: every tensor keeps its buffer, results repeat
+    ex = T.TfliteExecutor(ctx, m)
+    try:
+        ex.set_input(x)
+        ex.run()
+        first = ex.output()
+        owned = len(ex.owned)
+        ex.set_input(rnd(n, hw, hw, c0))
+        ex.run()
+        ex.set_input(x)
+        ex.run()
+        assert len(ex.owned) == owned, "run() allocated new buffers"
+        assert len(ex.op_log) == len(m.operators)
+        assert ex.output().tobytes() == first.tobytes()
+        assert_close(first, ref.reshape(-1), 1e-4, 1e-4, "small cnn probs (executor reuse)")
+    finally:
+        ex.close()
 
 
 def test_mobilenet_v2_export_roundtrip(ctx):
