@@ -119,6 +119,17 @@ int shp_launch_ex(shp_ctx* ctx, const char* kernel, const void* in0, const void*
                   const int32_t* push, size_t n_push, uint64_t out_elems,
                   const shp_epilogue* epi);
 
+/* As shp_launch_ex, but allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot call hipMalloc (code under stream capture, tight serving loops,
+ * harnesses that forbid allocation).  The dense kernels' split-K partials and tile counters
+ * live in one fixed 64 MiB device array per GPU (held until the process ends) instead of the
+ * context workspace; a launch whose plan needs more returns SHP_ERR_UNSUPPORTED before
+ * anything runs.  Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other contexts, other threads) race.  Per-launch timing does not apply. */
+int shp_launch_static(shp_ctx* ctx, const char* kernel, const void* in0, const void* in1,
+                      void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
+                      const shp_epilogue* epi);
+
 /* Host-to-host synchronous call with the semantics of
  * run_kernel(device_selector, &KernelRun) (source/tflite_loader/src/vulkan.rs:42-44):
  * upload in0[n0], in1[n1], dispatch, wait, download out[n_out].  grid_hint (the

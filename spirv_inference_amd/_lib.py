@@ -81,6 +81,9 @@ SIGNATURES = [
     ("shp_launch_ex", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.POINTER(C.c_int32), C.c_size_t, C.c_uint64,
                                 C.POINTER(Epilogue)]),
+    ("shp_launch_static", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                    C.POINTER(C.c_int32), C.c_size_t, C.c_uint64,
+                                    C.POINTER(Epilogue)]),
     ("shp_run_kernel", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                  C.c_size_t, C.c_void_p, C.c_size_t, C.POINTER(C.c_int32),
                                  C.c_size_t, C.c_uint32, C.POINTER(RunInfo)]),

@@ -187,6 +187,8 @@ int shp_create(const char* selector, shp_ctx** out) {
         dev = (int)v;
     }
     SHP_HIP_CHECK(hipSetDevice(dev));
+    int arc = shp::static_scratch_attach(dev);
+    if (arc) return arc;
     Ctx* c = new Ctx();
     c->device = dev;
     hipError_t se = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);

@@ -40,4 +40,8 @@ struct Ctx {
     int collect_timing();
 };
 
+// Resolves, once per device and with that device current, the device address of the fixed
+// split-K scratch array behind shp_launch_static (static_scratch.hip).
+int static_scratch_attach(int device);
+
 }  // namespace shp
