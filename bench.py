@@ -117,6 +117,39 @@ def time_alternating_steps(ctx, m, steps: int, warmup: int, batch: int, streams:
             c.close()
 
 
+def time_hlo_module(ctx, m, steps: int, warmup: int, batch: int):
+    """The same step through the HLO path: the generated ResNet-50 v1.5 HLO text module,
+    parsed, compiled (hlo_program) on the graph's own weights and input, replayed from a
+    hipGraph K times (host clock).  Its output must equal the C++ graph's bit for bit."""
+    from spirv_inference_amd import hlo_exec as X
+    from spirv_inference_amd import hlo_gen as G
+    from spirv_inference_amd.hlo_program import HloProgram
+    text, spec = G.resnet50_v15(batch)
+    ops = X.parse_hlo_text(text)
+    m.use_graph(False)
+    m.run()
+    ctx.sync()
+    want = m.output(0).download()
+    prog = HloProgram(X.DeviceBackend(ctx), ops, G.model_bindings(m, spec))
+    try:
+        for _ in range(max(warmup, 2)):
+            prog.run(graph=True)
+        ctx.sync()
+        identical = bool(np.array_equal(prog.read(0).reshape(-1), want))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            prog.run(graph=True)
+        ctx.sync()
+        elapsed = time.perf_counter() - t0
+        return dict(img_s=round(batch * steps / elapsed, 3),
+                    ms_per_step=round(elapsed / steps * 1e3, 4), hlo_ops=len(ops),
+                    launches=len(prog.launches), identical_to_cpp_graph=identical,
+                    region="generated ResNet-50 v1.5 HLO text -> parse_hlo_text -> hlo_program "
+                           "(fused epilogues / row kernels) -> one hipGraph, replayed K times")
+    finally:
+        prog.close()
+
+
 def bench_resnet(ctx, steps: int, warmup: int, batch: int, concurrency: int = 1):
     from spirv_inference_amd.models import Model
     m = Model(ctx, "resnet50_v1_5", batch, seed=2)
@@ -163,6 +196,7 @@ def bench_resnet(ctx, steps: int, warmup: int, batch: int, concurrency: int = 1)
         conv_avg_launch_ms=conv_ms / max(conv_n, 1), achieved_tflops=achieved,
         per_kernel_ms={k: v[0] / steps for k, v in sorted(rep.items())}, top1=top1,
         weight_bytes=wbytes, concurrent=None)
+    res["hlo_path"] = time_hlo_module(ctx, m, steps, warmup, batch)
     if concurrency > 1:
         img_s, ms, top1_c = time_alternating_steps(ctx, m, steps, warmup, batch, concurrency)
         res["concurrent"] = dict(streams=concurrency, img_s=round(img_s, 3),
@@ -329,6 +363,10 @@ def main() -> int:
     log(f"resnet50 b{args.batch} (one chain): {rn['img_s']:.1f} img/s, "
         f"{rn['ms_per_step']:.3f} ms/step (eager+events {rn['eager_ms_per_step']:.3f} ms), "
         f"conv {rn['achieved_tflops']:.1f} TFLOP/s")
+    hp = rn["hlo_path"]
+    log(f"resnet50 b{args.batch} via the HLO text module: {hp['img_s']:.1f} img/s "
+        f"({hp['launches']} launches for {hp['hlo_ops']} HLO ops; output identical to the "
+        f"C++ graph: {hp['identical_to_cpp_graph']})")
     if rn["concurrent"]:
         cc = rn["concurrent"]
         log(f"resnet50 b{args.batch}, {cc['streams']} steps in flight on {cc['streams']} "
@@ -433,6 +471,7 @@ def main() -> int:
             "profiled_region": f"K b{args.batch} steps launched eagerly on one stream with a "
                                "hipEvent pair per kernel (roofline source)",
             "concurrent": rn["concurrent"],
+            "hlo_path": rn["hlo_path"],
             "eager_ms_per_step": round(rn["eager_ms_per_step"], 4),
             "kernel_ms_per_step": round(rn["kernel_ms_per_step"], 4),
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},

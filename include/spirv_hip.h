@@ -138,6 +138,21 @@ int shp_run_kernel(shp_ctx* ctx, const char* kernel, const float* in0, size_t n0
                    const float* in1, size_t n1, float* out, size_t n_out, const int32_t* push,
                    size_t n_push, uint32_t grid_hint, shp_run_info* info);
 
+/* ---- captured launch sequences (hipGraph) ------------------------------------
+ * The reference records and submits a command buffer per dispatch
+ * (source/tflite_loader/src/vulkan.rs:132-171).  A caller that repeats one sequence of
+ * shp_launch* calls on a context records it once: between shp_capture_begin and
+ * shp_capture_end nothing runs, the launches are recorded; shp_graph_launch replays them
+ * on the context stream.  The recorded launches keep the device pointers they were given
+ * (tensors, the context's split-K workspace): run the sequence once eagerly before
+ * capturing so the workspace has its final size, and keep every tensor alive while the
+ * graph can be replayed.  Per-launch timing is not recorded inside a capture. */
+typedef struct shp_graph shp_graph;
+int shp_capture_begin(shp_ctx* ctx);
+int shp_capture_end(shp_ctx* ctx, shp_graph** out);
+int shp_graph_launch(shp_graph* graph);
+void shp_graph_destroy(shp_graph* graph);
+
 /* ---- per-launch timing (the reference's KernelOutput.elapsed_ms, vulkan.rs:163-171) */
 /* When enabled, every launch is bracketed by hipEvents on the context stream and
  * accumulated per kernel name. */
@@ -229,7 +244,9 @@ int shp_llama_engine(shp_llama* lm, int* engine);
 int shp_llama_logits(shp_llama* lm, void** dptr, uint64_t* elems);
 /* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head"
  * [vocab,hidden], or per layer "attn_norm", "wqkv" (rows q | k | v), "wo", "ffn_norm",
- * "w_gate_up" (rows interleaved: 2n = gate n, 2n+1 = up n), "w_down".
+ * "w_gate_up" (rows interleaved: 2n = gate n, 2n+1 = up n), "w_down", and the layer's KV
+ * cache "k_cache" / "v_cache" [n_kv_heads][max_seq][head_dim] (rows < the current position
+ * are valid).
  * Projection matrices are stored row-major [out,in], the transpose of export_llama.py's
  * [in,out] (`.T` at :203-217,238): one output's weights are contiguous for the GEMV. */
 int shp_llama_weight(shp_llama* lm, int32_t layer, const char* which, void** dptr,

@@ -667,7 +667,7 @@ static const char* kNames[] = {
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
     "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
     "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
-    "hlo_reduce"};
+    "hlo_reduce", "hlo_strided_copy"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -970,6 +970,29 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
             h_unravel(idx, od, r, oc);
             for (int i = 0; i < r; ++i) sc[perm[i]] = oc[i];
             out[idx] = in0[h_ravel(sc, sd, r)];
+        }
+        return 0;
+    }
+    if (!strcmp(name, "hlo_strided_copy")) { /* no reference counterpart: a view of the
+                                                 compiled HLO program made contiguous */
+        NEED(2);
+        int r = push[0];
+        if (r < 1 || r > HMAX) return orc_fail(-4, "hlo_strided_copy: rank");
+        NEED(2 + 2 * r);
+        const int32_t *od = push + 2, *st = push + 2 + r;
+        if (!h_dims_ok(od, r) || h_elems(od, r) != push[1]) return orc_fail(-4, "hlo_strided_copy: dims");
+        TOTAL(push[1]);
+        int64_t extent = 1;
+        for (int k = 0; k < r; ++k) {
+            if (st[k] < 0) return orc_fail(-4, "hlo_strided_copy: negative stride");
+            extent += (int64_t)(od[k] - 1) * st[k];
+        }
+        if (n0 > 0 && extent > (int64_t)n0) return orc_fail(-4, "hlo_strided_copy: view exceeds in0");
+        for (int64_t idx = 0; idx < (int64_t)n_out; ++idx) {
+            int64_t oc[HMAX], off = 0;
+            h_unravel(idx, od, r, oc);
+            for (int k = 0; k < r; ++k) off += oc[k] * st[k];
+            out[idx] = in0[off];
         }
         return 0;
     }

@@ -87,6 +87,10 @@ SIGNATURES = [
     ("shp_run_kernel", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                  C.c_size_t, C.c_void_p, C.c_size_t, C.POINTER(C.c_int32),
                                  C.c_size_t, C.c_uint32, C.POINTER(RunInfo)]),
+    ("shp_capture_begin", C.c_int, [C.c_void_p]),
+    ("shp_capture_end", C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
+    ("shp_graph_launch", C.c_int, [C.c_void_p]),
+    ("shp_graph_destroy", None, [C.c_void_p]),
     ("shp_timing_enable", C.c_int, [C.c_void_p, C.c_int]),
     ("shp_timing_reset", C.c_int, [C.c_void_p]),
     ("shp_timing_entry", C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t,

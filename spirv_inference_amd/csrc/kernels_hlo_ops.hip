@@ -7,6 +7,7 @@
 //   compare (predicate as f32)    compiler.rs:511-537, binary_tensor :1521-1564, infer_broadcast_dims :1566-1572
 //   select                        compiler.rs:538-553, select_tensor :1574-1620
 //   reduce over any rank          compiler.rs:939-1007 (rank > 4 -> reduce_tensor :1730-1759), reduce_kind :1722-1728
+//   strided copy                  no counterpart: materialises a view of the compiled HLO program
 // The reference has no GLSL kernel (so no push layout) for these; the i32 push vectors
 // below carry the HLO attributes directly (shapes, `dimensions`, slice starts/limits/strides,
 // compare direction), so a host lowering passes what it parsed.  Ranks up to 8.
@@ -400,6 +401,31 @@ __global__ __launch_bounds__(kBlock) void reduce_nd_kernel(const float* __restri
     }
 }
 
+// ---- hlo_strided_copy: push {r, total, dims[r], strides[r]}: out (row-major over dims) =
+//      in0[sum_k c_k * strides[k]].  Materialises a strided view (a transpose, slice or
+//      broadcast the HLO program kept as a view) into a contiguous tensor; in0 points at the
+//      view's first element.  Strides >= 0 (0 on broadcast axes).
+int launch_strided_copy(const shp::Launch& l) {
+    const int32_t* q = l.push;
+    const int r = q[0];
+    if (r < 1 || r > kMaxRank) return shp::fail(SHP_ERR_SHAPE, "hlo_strided_copy: rank out of range 1..8");
+    if ((int64_t)l.n_push < 2 + 2 * r) return shp::fail(SHP_ERR_PUSH, "hlo_strided_copy needs 2 + 2*r push constants");
+    int dims[kMaxRank];
+    int rc = read_dims(q + 2, r, dims, "hlo_strided_copy");
+    if (rc) return rc;
+    if (elems_of(dims, r) != q[1]) return shp::fail(SHP_ERR_SHAPE, "hlo_strided_copy: total != product of dims");
+    rc = shp::check_total(l, q[1], "hlo_strided_copy");
+    if (rc) return rc;
+    Gather g{};
+    g.r = r;
+    for (int k = 0; k < r; ++k) {
+        if (q[2 + r + k] < 0) return shp::fail(SHP_ERR_SHAPE, "hlo_strided_copy: negative stride");
+        g.dims[k] = dims[k];
+        g.stride[k] = q[2 + r + k];
+    }
+    return launch_gather(l, g);
+}
+
 int launch_reduce_nd(const shp::Launch& l) {
     const int32_t* q = l.push;
     const int r = q[1];
@@ -448,6 +474,7 @@ KernelEntry kHloOpKernels[] = {
     {"hlo_compare", 5, false, launch_compare_select<false>},
     {"hlo_select", 4, false, launch_compare_select<true>},
     {"hlo_reduce", 4, false, launch_reduce_nd},
+    {"hlo_strided_copy", 2, false, launch_strided_copy},
 };
 const int kHloOpKernelCount = sizeof(kHloOpKernels) / sizeof(kHloOpKernels[0]);
 

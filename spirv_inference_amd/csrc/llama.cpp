@@ -454,6 +454,9 @@ int shp_llama_weight(shp_llama* p, int32_t layer, const char* which, void** dptr
     if (w == "ffn_norm") { *dptr = L.ffn_norm; *elems = H; return SHP_OK; }
     if (w == "w_gate_up") { *dptr = L.w_gu; *elems = 2 * F * H; return SHP_OK; }
     if (w == "w_down") { *dptr = L.w_down; *elems = H * F; return SHP_OK; }
+    const uint64_t cache_layer = (uint64_t)c.n_kv_heads * c.max_seq * c.head_dim;
+    if (w == "k_cache") { *dptr = lm->k_cache + layer * cache_layer; *elems = cache_layer; return SHP_OK; }
+    if (w == "v_cache") { *dptr = lm->v_cache + layer * cache_layer; *elems = cache_layer; return SHP_OK; }
     return fail(SHP_ERR_INVALID, "shp_llama_weight: unknown tensor '" + w + "'");
 }
 

@@ -413,6 +413,65 @@ int shp_run_kernel(shp_ctx* ctx, const char* kernel, const float* in0, size_t n0
     return rc;
 }
 
+// ---- captured launch sequences (hipGraph) --------------------------------------------
+// The reference re-records and resubmits a command buffer per dispatch (vulkan.rs:132-171);
+// a caller that repeats one launch sequence records it once and replays it.
+struct shp_graph {
+    Ctx* ctx;
+    hipStream_t stream;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+int shp_capture_begin(shp_ctx* ctx) {
+    if (!ctx) return fail(SHP_ERR_INVALID, "shp_capture_begin: null ctx");
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    SHP_HIP_CHECK(hipSetDevice(c->device));
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SHP_HIP_CHECK(hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(SHP_ERR_INVALID, "shp_capture_begin: the context stream is already capturing");
+    SHP_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->timing_before_capture = c->timing;
+    c->timing = false;  // no event records inside the capture
+    return SHP_OK;
+}
+
+int shp_capture_end(shp_ctx* ctx, shp_graph** out) {
+    if (!ctx || !out) return fail(SHP_ERR_INVALID, "shp_capture_end: null argument");
+    *out = nullptr;
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    c->timing = c->timing_before_capture;
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(SHP_ERR_HIP, std::string("shp_capture_end: ") + hipGetErrorString(e));
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(SHP_ERR_HIP, std::string("shp_capture_end: instantiate: ") + hipGetErrorString(e));
+    }
+    *out = new shp_graph{c, c->stream, g, x};
+    return SHP_OK;
+}
+
+int shp_graph_launch(shp_graph* g) {
+    if (!g) return fail(SHP_ERR_INVALID, "shp_graph_launch: null graph");
+    SHP_HIP_CHECK(hipGraphLaunch(g->exec, g->ctx->stream));
+    return SHP_OK;
+}
+
+void shp_graph_destroy(shp_graph* g) {
+    if (!g) return;
+    (void)hipStreamSynchronize(g->ctx->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 int shp_timing_enable(shp_ctx* ctx, int enable) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_timing_enable: null ctx");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);

@@ -29,6 +29,7 @@ struct Ctx {
         std::string name;
     };
     bool timing = false;
+    bool timing_before_capture = false;  // restored by shp_capture_end
     std::vector<Timer> timers;
     size_t timer_used = 0;
     std::map<std::string, std::pair<double, uint64_t>> timing_totals;

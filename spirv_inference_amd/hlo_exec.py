@@ -177,14 +177,38 @@ class DeviceBackend:
     def empty(self, n: int) -> DeviceTensor:
         return self.ctx.empty(max(1, n))
 
-    def launch(self, kernel: str, in0, in1, out, push: Sequence[int]) -> None:
-        self.ctx.launch(kernel, in0, in1, out, list(push))
+    def launch(self, kernel: str, in0, in1, out, push: Sequence[int], bias=None, residual=None,
+               act: int = 0, alpha: float = 0.0, out_elems: int | None = None) -> None:
+        self.ctx.launch(kernel, in0, in1, out, list(push), out_elems=out_elems, bias=bias,
+                        residual=residual, act=act, alpha=alpha)
+
+    def sub(self, t: DeviceTensor, offset: int, n: int) -> DeviceTensor:
+        """Elements [offset, offset + n) of `t` (no copy; `t` keeps the memory)."""
+        if offset == 0 and n == t.n:
+            return t
+        return DeviceTensor(self.ctx, n, ptr=t.ptr + 4 * int(offset), owned=False)
+
+    def write(self, t: DeviceTensor, offset: int, arr: np.ndarray) -> None:
+        self.sub(t, offset, arr.size).upload(arr)
 
     def read(self, t: DeviceTensor) -> np.ndarray:
         return t.download()
 
     def free(self, t: DeviceTensor) -> None:
         t.free()
+
+    # hipGraph capture of a launch sequence on the context stream
+    def capture_begin(self) -> None:
+        self.ctx.capture_begin()
+
+    def capture_end(self):
+        return self.ctx.capture_end()
+
+    def graph_launch(self, g) -> None:
+        g.launch()
+
+    def graph_destroy(self, g) -> None:
+        g.destroy()
 
 
 class HloExecutor:

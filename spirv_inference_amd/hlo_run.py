@@ -2,7 +2,9 @@
 
 Same flags as source/xla_hlo/src/main.rs:14-70 and a report of the same shape
 (:95-114: status, op_histogram, validation, execution, validate_only), but the module runs
-through spirv_inference_amd.hlo_exec: every op a kernel on resident device tensors.
+on resident device tensors: compiled by spirv_inference_amd.hlo_program (views, fused
+epilogues and row kernels, one launch list) by default, or op by op through
+spirv_inference_amd.hlo_exec with --op-by-op (the reference's own lowering, one kernel per op).
 
     python -m spirv_inference_amd.hlo_run --input model.txt --run \\
         --inputs-f32 p0.raw.f32,p1.raw.f32 --output-f32 out.raw.f32 \\
@@ -54,21 +56,34 @@ def validate(ops) -> dict:
 
 
 def run(ops, inputs: list[pathlib.Path], output: pathlib.Path | None,
-        expected: pathlib.Path | None, epsilon: float, device: str) -> dict:
+        expected: pathlib.Path | None, epsilon: float, device: str,
+        op_by_op: bool = False) -> dict:
+    from .hlo_program import HloProgram
     from .runtime import Context
     params = [np.asarray(read_raw_f32(p)) for p in inputs]
     with Context(device) as ctx:
-        ex = X.HloExecutor(X.DeviceBackend(ctx), ops)
         t0 = time.perf_counter()
-        out, shape = ex.run(params)
-        ctx.sync()
+        if op_by_op:
+            ex = X.HloExecutor(X.DeviceBackend(ctx), ops)
+            out, shape = ex.run(params)
+            ctx.sync()
+            y = out.download()
+            steps = len(ex.record)
+        else:
+            prog = HloProgram(X.DeviceBackend(ctx), ops, params)
+            prog.run()
+            ctx.sync()
+            y = prog.read(0).reshape(-1)
+            shape = prog.outputs()[0][1]
+            steps = len(prog.launches)
+            prog.close()
         ms = (time.perf_counter() - t0) * 1e3
-        y = out.download()
         dev = {"name": ctx.device_name, "vendor_id": ctx.vendor_id, "device_id": ctx.device_id}
     if output is not None:
         output.parent.mkdir(parents=True, exist_ok=True)
         y.astype("<f4").tofile(output)
-    res = {"status": "pass", "steps": len(ex.record), "output_shape": list(shape),
+    res = {"status": "pass", "steps": steps, "mode": "op_by_op" if op_by_op else "compiled",
+           "output_shape": list(shape),
            "output": {"path": str(output) if output else None, "elements": int(y.size),
                       "sha256": hashlib.sha256(y.astype("<f4").tobytes()).hexdigest()},
            "device": dev, "elapsed_ms": ms}
@@ -97,6 +112,8 @@ def main(argv=None) -> int:
     ap.add_argument("--output-f32", type=pathlib.Path)
     ap.add_argument("--expected-f32", type=pathlib.Path)
     ap.add_argument("--epsilon", type=float, default=1e-4)
+    ap.add_argument("--op-by-op", action="store_true",
+                    help="one kernel per HLO op (the reference's lowering) instead of compiling")
     a = ap.parse_args(argv)
     ops = X.parse_hlo_text(a.input.read_text())
     validation = validate(ops)
@@ -110,7 +127,8 @@ def main(argv=None) -> int:
         if validation["status"] != "pass":
             execution = {"status": "blocked", "reason": validation["reason"]}
         else:
-            execution = run(ops, inputs, a.output_f32, a.expected_f32, a.epsilon, a.device)
+            execution = run(ops, inputs, a.output_f32, a.expected_f32, a.epsilon, a.device,
+                            a.op_by_op)
     status = execution["status"] if execution["status"] in ("pass", "fail") else validation["status"]
     report = {"status": status, "input": str(a.input), "op_histogram": dict(Counter(o.opcode for o in ops)),
               "validation": validation, "execution": execution, "validate_only": a.validate_only}

@@ -150,6 +150,16 @@ class Context:
                                      C.byref(epi))
         check(rc, f"launch {kernel}")
 
+    # -- captured launch sequences
+    def capture_begin(self) -> None:
+        """Record (instead of run) the launches made on this context until capture_end()."""
+        check(lib().shp_capture_begin(self.handle), "shp_capture_begin")
+
+    def capture_end(self) -> "Graph":
+        g = C.c_void_p()
+        check(lib().shp_capture_end(self.handle, C.byref(g)), "shp_capture_end")
+        return Graph(g.value)
+
     def run_kernel(self, spec: KernelRun) -> KernelOutput:
         """Synchronous host-to-host call with the semantics of vulkan.rs:42-44."""
         a0 = np.ascontiguousarray(spec.input0, dtype=np.float32).reshape(-1)
@@ -182,6 +192,21 @@ class Context:
             out[name.value.decode()] = (ms.value, cnt.value)
             i += 1
         return out
+
+
+class Graph:
+    """A recorded launch sequence (shp_graph): launch() replays it on the context stream."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    def launch(self) -> None:
+        check(lib().shp_graph_launch(self.handle), "shp_graph_launch")
+
+    def destroy(self) -> None:
+        if self.handle:
+            lib().shp_graph_destroy(self.handle)
+            self.handle = None
 
 
 def kernel_names() -> list[str]:

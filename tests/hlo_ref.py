@@ -33,8 +33,17 @@ class OracleBackend:
     def empty(self, n):
         return np.zeros(max(1, n), np.float32)
 
-    def launch(self, kernel, in0, in1, out, push):
-        out[:] = orc.run(kernel, in0, in1, out.size, list(push), out_init=out)
+    def launch(self, kernel, in0, in1, out, push, bias=None, residual=None, act=0, alpha=0.0,
+               out_elems=None):
+        n = out.size if out_elems is None else out_elems
+        out[:n] = orc.run(kernel, in0, in1, n, list(push), bias=bias, residual=residual,
+                          act=act, alpha=alpha, out_init=out[:n])
+
+    def sub(self, t, offset, n):
+        return t[offset:offset + n]
+
+    def write(self, t, offset, arr):
+        t[offset:offset + arr.size] = arr
 
     def read(self, t):
         return t
@@ -78,8 +87,9 @@ def _conv_nhwc(x, w, stride, pads):
     return y
 
 
-def eval_numpy(ops, params):
-    """float64 evaluation with XLA semantics; returns the last op's value."""
+def eval_numpy(ops, params, all_values=False):
+    """float64 evaluation with XLA semantics; returns the last op's value (all_values: the
+    dict of every value; a tuple ROOT's elements are then looked up by name)."""
     v, last = {}, None
     for op in ops:
         a = [v[o] for o in op.operands if o in v]
@@ -162,4 +172,4 @@ def eval_numpy(ops, params):
             raise NotImplementedError(oc)
         v[op.result] = np.asarray(r, np.float64)
         last = op.result
-    return v[last]
+    return v if all_values else v[last]

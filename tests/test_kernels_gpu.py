@@ -566,6 +566,17 @@ def test_hlo_slice(ctx, orc, shape, starts, limits, strides):
                                   orc.run("hlo_slice", x, None, n, push))
 
 
+@pytest.mark.parametrize("base,offset,shape,strides", [
+    (2 * 3 * 4 * 5, 0, (2, 4, 3, 5), (60, 5, 20, 1)),
+    (8 * 128 * 2304, 768, (8, 12, 128, 64), (128 * 2304, 64, 2304, 1)),
+    (4 * 64, 0, (4, 8, 64), (64, 0, 1)), (30, 3, (4, 3), (6, 2))])
+def test_hlo_strided_copy(ctx, orc, base, offset, shape, strides):
+    x = rnd(base)
+    n, push = int(np.prod(shape)), [len(shape), int(np.prod(shape)), *shape, *strides]
+    np.testing.assert_array_equal(_dev(ctx, "hlo_strided_copy", x[offset:], None, n, push),
+                                  orc.run("hlo_strided_copy", x[offset:], None, n, push))
+
+
 def test_hlo_concatenate(ctx, orc):
     """Rotate-half's concatenate (two halves on the last axis) and a three-way axis-1 join."""
     from spirv_inference_amd import hlo_ops as H

@@ -162,3 +162,22 @@ def test_errors_fail_closed():
         orc.run("hlo_transpose", r32(4), None, 4, [2, 4, 2, 2, 0, 0])
     with pytest.raises(RuntimeError):  # source dim does not match its output axis
         orc.run("hlo_broadcast", r32(3), None, 8, H.broadcast_push((3,), (2, 4), (1,)))
+
+
+@pytest.mark.parametrize("base_shape,offset,shape,strides", [
+    ((2, 3, 4, 5), 0, (2, 4, 3, 5), (60, 5, 20, 1)),          # transpose {0,2,1,3}
+    ((8, 16, 2304), 768, (8, 12, 16, 64), (16 * 2304, 64, 2304, 1)),  # BERT head view of k
+    ((4, 64), 0, (4, 8, 64), (64, 0, 1)),                      # broadcast axis (stride 0)
+    ((30,), 3, (4, 3), (6, 2)),                                # offset + stepped slice
+])
+def test_oracle_strided_copy_is_numpy_as_strided(base_shape, offset, shape, strides):
+    base = r32(*base_shape).reshape(-1)
+    view = np.lib.stride_tricks.as_strided(base[offset:], shape, [s * 4 for s in strides])
+    push = [len(shape), int(np.prod(shape)), *shape, *strides]
+    got = orc.run("hlo_strided_copy", base[offset:], None, int(np.prod(shape)), push)
+    np.testing.assert_array_equal(got, view.reshape(-1))
+
+
+def test_oracle_strided_copy_rejects_a_view_past_its_input():
+    with pytest.raises(RuntimeError, match="exceeds"):
+        orc.run("hlo_strided_copy", r32(10), None, 12, [2, 12, 3, 4, 4, 1])
