@@ -174,7 +174,8 @@ int shp_model_create(shp_ctx* ctx, const char* arch, int32_t batch, int32_t seq_
 void shp_model_destroy(shp_model* model);
 /* Enqueue one forward pass of every op on the context stream. */
 int shp_model_run(shp_model* model);
-/* Capture the op list into a hipGraph once and replay it on later runs. */
+/* Capture the op list into a hipGraph once and replay it on later runs; disabling releases
+ * the capture, so the next enable records the op list again. */
 int shp_model_use_graph(shp_model* model, int enable);
 int shp_model_input(shp_model* model, int index, void** dptr, uint64_t* elems);
 int shp_model_output(shp_model* model, int index, void** dptr, uint64_t* elems);

@@ -1089,10 +1089,44 @@ double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps
     return cost;
 }
 
+// Plans measured best on MI355X for the benchmark configs' shapes (sweeps of every tile, K
+// tile, split count and prefetch depth per shape, interleaved A/B against the cost model);
+// the cost model decides every other shape.  Key: operand mode, M, N, K, and for
+// convolutions the input channels, stride and kernel height (0 = any).
+struct TunedPlan {
+    int amode, M, N, K, cic, csh, ckh;
+    TileCfg t;
+    int splits;
+};
+const TunedPlan kTuned[] = {
+    // BERT-base b8 s128 (hlo_dot_rank2: row-major A and B)
+    {shp::A_KVEC, 1024, 2304, 768, 0, 0, 0, {64, 64, 32, false, 2}, 2},
+    {shp::A_KVEC, 1024, 768, 768, 0, 0, 0, {64, 64, 32, false, 2}, 1},
+    {shp::A_KVEC, 1024, 3072, 768, 0, 0, 0, {64, 64, 32, false, 2}, 1},
+    {shp::A_KVEC, 1024, 768, 3072, 0, 0, 0, {64, 64, 32, false, 2}, 4},
+};
+
+bool tuned_plan(const GemmParams& p, int nbatch, int amode, bool hot, Plan* out) {
+    if (nbatch != 1 || !hot) return false;
+    for (const TunedPlan& e : kTuned) {
+        if (e.amode != amode || e.M != p.M || e.N != p.N || e.K != p.K) continue;
+        if (e.cic && (e.cic != p.cic || e.csh != p.csh || e.ckh != p.ckh)) continue;
+        int kps = ((p.K + e.splits - 1) / e.splits + 31) / 32 * 32;
+        if ((p.K + kps - 1) / kps != e.splits) return false;
+        *out = Plan{e.t, e.splits, kps};
+        return true;
+    }
+    return false;
+}
+
 Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv_a,
-               const shp::GemmTune& tn) {
+               const shp::GemmTune& tn, int amode = -1) {
     static const int kTiles[5][2] = {{128, 128}, {128, 64}, {64, 64}, {128, 128}, {128, 64}};
     static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 12, 16};
+    Plan tuned;
+    if (tn.table >= 0 && !tn.tile && !tn.bk && !tn.splits && !tn.dma && !tn.pg && amode >= 0 &&
+        tuned_plan(p, nbatch, amode, hot, &tuned))
+        return tuned;
     if (dma_ok && conv_a && tn.dma == 0 && !tn.splits && dma_preferred(p, nbatch))
         return Plan{{128, 64, 16, true}, 1, ((p.K + 31) / 32) * 32};
     Plan best{{128, 128, 32, false}, 1, 0};
@@ -1137,7 +1171,7 @@ size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode
     int nbatch = p.batch_outer * p.batch_inner;
     Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
                         dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4,
-                        tune ? *tune : kAuto);
+                        tune ? *tune : kAuto, amode);
     if (pl.splits <= 1) return 0;
     return kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
 }
@@ -1192,7 +1226,7 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     const bool fix_ok = cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 && (p.N & 3) == 0 &&
                         (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
                         (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual));
-    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn);
+    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn, amode);
     size_t need = pl.splits > 1
                       ? kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float)
                       : 0;

@@ -506,7 +506,15 @@ int shp_model_run(shp_model* model) {
 
 int shp_model_use_graph(shp_model* model, int enable) {
     if (!model) return fail(SHP_ERR_INVALID, "shp_model_use_graph: null model");
-    reinterpret_cast<Model*>(model)->use_graph = enable != 0;
+    Model* m = reinterpret_cast<Model*>(model);
+    m->use_graph = enable != 0;
+    if (!enable && m->exec) {  // a later enable captures again (with the current planner state)
+        (void)hipStreamSynchronize(m->ctx->stream);
+        (void)hipGraphExecDestroy(m->exec);
+        (void)hipGraphDestroy(m->graph);
+        m->exec = nullptr;
+        m->graph = nullptr;
+    }
     return SHP_OK;
 }
 
