@@ -259,6 +259,35 @@ def test_depthwise(ctx, orc, k, s, c, n, hw):
     assert_close(y, r, 1e-4, 1e-4, "dw nchw")
 
 
+@pytest.mark.parametrize("k,s,dil,c,n,h,w", [(3, 1, 2, 20, 2, 15, 13), (5, 2, 1, 100, 3, 17, 30),
+                                             (3, 2, 1, 36, 1, 7, 7), (5, 1, 1, 4, 1, 9, 11),
+                                             (3, 1, 1, 64, 1, 8, 8)])
+def test_depthwise_nhwc_lds_tiles(ctx, orc, k, s, dil, c, n, h, w):
+    """The LDS-tiled NHWC kernel on ragged tiles (output sizes not multiples of 8, channel
+    counts not multiples of 32), dilation, stride 2 and a 5x5 window, with residual + ReLU6:
+    against the oracle, and bit for bit against the untiled kernel."""
+    from spirv_inference_amd._lib import check, lib
+    oh, ow = -(-h // s), -(-w // s)
+    pt = max((oh - 1) * s + (k - 1) * dil + 1 - h, 0) // 2
+    pl = max((ow - 1) * s + (k - 1) * dil + 1 - w, 0) // 2
+    total = n * oh * ow * c
+    push = [n, c, h, w, oh, ow, k, k, s, s, 1, pt, pl, dil, dil, total]
+    x = rnd(n, h, w, c)
+    wt = np.concatenate([rnd(k * k * c, scale=0.3), rnd(c)])
+    res = rnd(total)
+    r = orc.run("depthwise_conv2d_nhwc", x, wt, total, push, residual=res, act="relu6")
+    ys = {}
+    try:
+        for mode in (1, -1):  # forced tiled / untiled
+            check(lib().shp_tune(ctx.handle, b"dw_tile", mode), "tune")
+            ys[mode] = hip(ctx, "depthwise_conv2d_nhwc", x, wt, total, push, residual=res,
+                           act="relu6")
+    finally:
+        check(lib().shp_tune(ctx.handle, b"dw_tile", 0), "tune")
+    assert_close(ys[1], r, 1e-4, 1e-4, "dw nhwc tiles")
+    np.testing.assert_array_equal(ys[1], ys[-1])
+
+
 def test_resize_bilinear(ctx, orc):
     x = rnd(2, 3, 17, 13)
     for ac, hp in [(1, 0), (0, 1), (0, 0)]:
