@@ -70,6 +70,28 @@ def measured_conv_traffic(batch: int):
     return None
 
 
+def measured_config_hbm(name: str):
+    """Per-family kernel time and HBM bytes of one latency config, from the committed
+    rocprofv3 summary profiles/<name>.md (kernel trace + FETCH_SIZE / WRITE_SIZE passes of
+    an eager forward): {registry kernel: {us, hbm_gbs, frac_hbm, hbm_over_alg}}."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    if not os.path.exists(path):
+        return None
+    out, in_hbm = {}, False
+    for ln in open(path):
+        if ln.startswith("## HBM traffic"):
+            in_hbm = True
+            continue
+        if ln.startswith("## ") and in_hbm:
+            break
+        if in_hbm and ln.startswith("| `"):
+            c = [x.strip() for x in ln.strip().strip("|").split("|")]
+            out[c[0].strip("`")] = {"us": float(c[2]), "hbm_gbs": float(c[5]),
+                                    "frac_hbm": round(float(c[5]) / PEAK_HBM_GBS, 4),
+                                    "hbm_over_alg": float(c[8])}
+    return out or None
+
+
 def measured_decode_traffic(n_prompt: int, n_new: int):
     """HBM bytes per token of the persistent decode from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (profiles/tinyllama_decode_persistent.md: 32-token prompt, 20 new
@@ -477,6 +499,11 @@ def main() -> int:
             "per_kernel_ms_per_step": {k: round(v, 4) for k, v in rn["per_kernel_ms"].items()},
             "top1": rn["top1"],
             "configs": configs,
+            "configs_hbm_by_kernel": {k: measured_config_hbm(f) for k, f in (
+                ("mobilenet_v2", "mobilenet_v2_b1"), ("efficientnet_lite0", "efficientnet_lite0_b8"),
+                ("bert_base", "bert_base_b8_s128"))},
+            "configs_hbm_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE of an eager forward per config, "
+                                  "profiles/<config>.md",
         },
     }
     if dec is not None:
