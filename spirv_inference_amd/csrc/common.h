@@ -29,9 +29,11 @@ int fail(int code, const std::string& msg);
 // tile 1: 128x128, 2: 128x64, 3: 64x64; bk 16 or 32; splits: split-K count; dma 0 automatic,
 // -1 never, 1: 128x128, 2: 128x64 pipelined kernel; pg: register prefetch depth 1 or 2;
 // table: -1 ignores the measured per-shape plans (planner cost model only); dw: the NHWC
-// depthwise convolution with (1) or without (-1) its LDS tile instead of the automatic choice.
+// depthwise convolution with (1) or without (-1) its LDS tile instead of the automatic choice;
+// bl: the buffer-loaded GEMM kernel never (-1) or, where its operand forms allow it, always
+// (1); with bl 1, tile 1/2/3 and bk 16/32/64 pick its tile.
 struct GemmTune {
-    int tile = 0, bk = 0, splits = 0, dma = 0, pg = 0, table = 0, dw = 0;
+    int tile = 0, bk = 0, splits = 0, dma = 0, pg = 0, table = 0, dw = 0, bl = 0;
 };
 
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.

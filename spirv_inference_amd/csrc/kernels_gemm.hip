@@ -588,6 +588,257 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
                                               gridDim.z, (int64_t)bz * gridDim.x + blockIdx.x);
 }
 
+// ---- buffer-loaded variant (gemm_bl_kernel) for the row-contiguous operand forms of the
+// model paths: A = rows (A_KVEC) or an NHWC im2col whose K tile sits inside one (ky, kx) tap
+// (A_CONV_NHWC4 with IC % BK == 0); B = [K][N] (B_NVEC) or [N][K] (B_KVEC); K a multiple of
+// BK in every split.
+//
+// What makes it faster than gemm_mfma_kernel (measured on MI355X): every operand load is one
+// buffer_load_dwordx4 whose per-lane byte offset is computed once, outside the K loop, and
+// whose K advance is a scalar offset, so the loop issues no address arithmetic and no
+// bounds checks.  Rows past M and columns past N are clamped to the last one (their products
+// are never stored); a padding tap of a convolution gets an offset past the operand's range,
+// for which the buffer load returns zeros.  Each fragment step (four MFMA k-pairs) also
+// stores one register-staged chunk of the next K tile into the other LDS buffer and issues
+// one load of the tile after it (two tiles in flight), and the next step's fragments are read
+// before its MFMAs, so LDS and global latency overlap the MFMA stream instead of sitting
+// between dependent MFMAs.
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Raw dword buffer resource word 3 for gfx9-family devices.
+constexpr int kBufferWord3 = 0x00020000;
+// A byte offset beyond every operand range (the host keeps ranges <= 2 GiB): loads return 0.
+constexpr unsigned kOobOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base, int64_t elems) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(elems * 4), kBufferWord3);
+}
+
+__device__ __forceinline__ f4v buffer_load4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Elements an operand spans (per batch), as the buffer range of its loads.
+__device__ __host__ inline int64_t bl_a_extent(const GemmParams& p, int amode) {
+    if (amode == shp::A_CONV_NHWC4) return (int64_t)p.cn * p.cih * p.ciw * p.cic;
+    return (int64_t)(p.M - 1) * p.sam + p.K;
+}
+__device__ __host__ inline int64_t bl_b_extent(const GemmParams& p, int bmode) {
+    if (bmode == shp::B_KVEC) return (int64_t)(p.N - 1) * p.sbn + p.K;
+    return (int64_t)(p.K - 1) * p.sbk + p.N;
+}
+
+template <int BM, int BN, int BK, int AM, int BMD>
+__global__ __launch_bounds__(256) void gemm_bl_kernel(GemmParams p) {
+    static_assert(AM == shp::A_KVEC || AM == shp::A_CONV_NHWC4, "row-contiguous A");
+    static_assert(BMD == shp::B_NVEC || BMD == shp::B_KVEC, "row-contiguous B");
+    constexpr int FM = BM / 64, FN = BN / 64;           // 2x2 waves of FM x FN 32x32 blocks
+    constexpr int KQ = BK / 4;                           // float4 chunks per K row of a tile
+    constexpr int NA = BM * BK / 1024, NB = BK * BN / 1024, NE = NA + NB;
+    constexpr int NS = BK / 8;                           // fragment steps per K tile
+    constexpr bool BT = BMD == shp::B_KVEC;              // B tile stored [n][k] (else [k][n])
+    constexpr int AS = BK + 4;                           // row stride of K-contiguous tiles
+    constexpr int BS = BT ? AS : BN + 4;                 // row stride of the B tile
+    constexpr int ABUF = BM * AS;
+    constexpr int BBUF = BT ? BN * AS : BK * BS;
+    constexpr int SMEM = 2 * (ABUF + BBUF);
+    constexpr int CS = BN + 4;
+    constexpr int RC = BM * CS <= SMEM ? BM : (BM / 2) * CS <= SMEM ? BM / 2 : 32;
+    constexpr int TPR = BN / 4;                          // threads per [k][n] B row
+    static_assert(FM >= 1 && FN >= 1 && NA >= 1 && NB >= 1 && NS >= 2, "tile shape");
+    static_assert(RC >= 32 && BM % RC == 0, "epilogue chunk must hold whole 32-row blocks");
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+    float* const As = smem;
+    float* const Bs = smem + 2 * ABUF;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 31, lh = lane >> 5;
+
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int ntiles = tiles_m * tiles_n;
+    int bid = blockIdx.x;
+    const int full = (ntiles / 8) * 8;
+    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
+    const int m0 = (bid / tiles_n) * BM, n0 = (bid % tiles_n) * BN;
+
+    const int split = blockIdx.y;
+    const int bz = blockIdx.z;
+    const int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
+    const float* A = p.a + bo * p.sa_outer + bi * p.sa_inner;
+    const float* B = p.b + bo * p.sb_outer + bi * p.sb_inner;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int ntk = kend > kbeg ? (kend - kbeg) / BK : 0;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, bl_a_extent(p, AM));
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, bl_b_extent(p, BMD));
+
+    // ---- loop-invariant per-lane load offsets
+    const int ka = (tid % KQ) * 4;  // k of this lane's A (and K-contiguous B) chunk
+    // A_KVEC: byte offset of the chunk at kbeg.  A_CONV_NHWC4: element offset of the row's
+    // tap (0, 0), channel ka (negative where the window starts in the padding), and the
+    // window origin for the per-tap range check.
+    int aoff[NA], iy0[AM == shp::A_CONV_NHWC4 ? NA : 1], ix0[AM == shp::A_CONV_NHWC4 ? NA : 1];
+#pragma unroll
+    for (int e = 0; e < NA; ++e) {
+        const int m = m0 + tid / KQ + (256 / KQ) * e;
+        if constexpr (AM == shp::A_KVEC) {
+            aoff[e] = (int)(((int64_t)min(m, p.M - 1) * p.sam + kbeg + ka) * 4);
+        } else {
+            const ConvRow r = conv_row(p, m, AM);
+            aoff[e] = (int)r.base + ka;
+            iy0[e] = r.valid ? r.iy0 : -(1 << 28);  // rows past M fail every range check
+            ix0[e] = r.ix0;
+        }
+    }
+    // 1x1 convolutions without padding read every row in range: the tap is fixed and the
+    // channel advance is a scalar offset, as for A_KVEC.
+    const bool tap1 = AM == shp::A_CONV_NHWC4 && p.ckh == 1 && p.ckw == 1 && p.cpt == 0 &&
+                      p.cpl == 0;
+    unsigned boff[NB];
+#pragma unroll
+    for (int e = 0; e < NB; ++e) {
+        if constexpr (BT) {
+            const int n = min(n0 + tid / KQ + (256 / KQ) * e, p.N - 1);
+            boff[e] = (unsigned)(((int64_t)n * p.sbn + kbeg + ka) * 4);
+        } else {
+            const int kr = tid / TPR + (256 / TPR) * e;
+            const int n = min(n0 + (tid % TPR) * 4, p.N - 4);
+            boff[e] = (unsigned)(((int64_t)(kbeg + kr) * p.sbk + n) * 4);
+        }
+    }
+    const unsigned b_step = BT ? BK * 4u : (unsigned)(BK * p.sbk * 4);
+
+    struct Stage { f4v e[NE]; };
+    auto load_e = [&](int kt, Stage& s, int e) __attribute__((always_inline)) {
+        if (e < NA) {
+            if constexpr (AM == shp::A_KVEC) {
+                s.e[e] = buffer_load4(ra, (unsigned)aoff[e], (unsigned)(kt * BK * 4));
+            } else if (tap1) {
+                const unsigned v = iy0[e] >= 0 ? (unsigned)aoff[e] * 4u : kOobOffset;
+                s.e[e] = buffer_load4(ra, v, (unsigned)((kbeg + kt * BK) * 4));
+            } else {
+                // K tile kt lies inside tap (ky, kx), channels ic0 .. ic0 + BK - 1
+                const int k0 = kbeg + kt * BK;
+                const int ic0 = k0 % p.cic, t = k0 / p.cic;
+                const int kx = t % p.ckw, ky = t / p.ckw;
+                const bool ok = (unsigned)(iy0[e] + ky) < (unsigned)p.cih &&
+                                (unsigned)(ix0[e] + kx) < (unsigned)p.ciw;
+                const int off = aoff[e] + (ky * p.ciw + kx) * p.cic + ic0;
+                s.e[e] = buffer_load4(ra, ok ? (unsigned)off * 4u : kOobOffset, 0u);
+            }
+        } else {
+            s.e[e] = buffer_load4(rb, boff[e - NA], (unsigned)kt * b_step);
+        }
+    };
+    auto store_e = [&](int buf, const Stage& s, int e) __attribute__((always_inline)) {
+        if (e < NA) {
+            *reinterpret_cast<f4v*>(&As[buf * ABUF + (tid / KQ + (256 / KQ) * e) * AS + ka]) = s.e[e];
+        } else if constexpr (BT) {
+            *reinterpret_cast<f4v*>(&Bs[buf * BBUF + (tid / KQ + (256 / KQ) * (e - NA)) * AS + ka]) =
+                s.e[e];
+        } else {
+            *reinterpret_cast<f4v*>(
+                &Bs[buf * BBUF + (tid / TPR + (256 / TPR) * (e - NA)) * BS + (tid % TPR) * 4]) = s.e[e];
+        }
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Fragments of one step: lanes 0-31 feed k = s of the tile, lanes 32-63 k = BK/2 + s (A and
+    // B agree, so any assignment of the tile's k to MFMA k-pairs works), so each lane reads four
+    // consecutive k of its A row (and, from a [n][k] tile, of its B column) at once.
+    const int arow = wm * (BM / 2) + li;
+    const int bcol = wn * (BN / 2) + li;
+    struct Frag { f4v a[FM]; f4v b[FN]; };
+    auto read = [&](int buf, int s4, Frag& f) __attribute__((always_inline)) {
+        const int kk = lh * (BK / 2) + s4 * 4;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+            f.a[fm] = *reinterpret_cast<const f4v*>(&As[buf * ABUF + (arow + fm * 32) * AS + kk]);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            if constexpr (BT) {
+                f.b[fn] = *reinterpret_cast<const f4v*>(&Bs[buf * BBUF + (bcol + fn * 32) * AS + kk]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) f.b[fn][q] = Bs[buf * BBUF + (kk + q) * BS + bcol + fn * 32];
+            }
+        }
+    };
+    auto mma = [&](const Frag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    acc[fm][fn] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[fm][q], f.b[fn][q], acc[fm][fn], 0, 0, 0);
+    };
+    // One K tile from LDS buffer `buf`; `wr` (the next tile) goes into buffer buf^1 chunk by
+    // chunk when `do_store`, and tile `ld_kt` is loaded into `ld` chunk by chunk.  The
+    // scheduling fences keep each step's memory instructions ahead of its MFMAs.
+    auto tile = [&](int buf, const Stage& wr, bool do_store, Stage& ld, int ld_kt)
+                    __attribute__((always_inline)) {
+        Frag f0, f1;
+        read(buf, 0, f0);
+#pragma unroll
+        for (int s4 = 0; s4 < NS; ++s4) {
+            const int e0 = s4 * NE / NS, e1 = (s4 + 1) * NE / NS;
+            if (s4 + 1 < NS) {
+                if (s4 & 1) read(buf, s4 + 1, f0);
+                else read(buf, s4 + 1, f1);
+            }
+            if (do_store)
+#pragma unroll
+                for (int e = e0; e < e1; ++e) store_e(buf ^ 1, wr, e);
+#pragma unroll
+            for (int e = e0; e < e1; ++e) load_e(ld_kt, ld, e);
+            if (s4 & 1) mma(f1);
+            else mma(f0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    if (ntk > 0) {
+        // Tile t lives in LDS buffer t & 1; register set s0 / s1 holds tile t + 1 and t + 2
+        // alternately.  The last two loads re-read the final tile (unused) so every set is
+        // redefined each iteration.
+        Stage s0, s1;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) load_e(0, s0, e);
+#pragma unroll
+        for (int e = 0; e < NE; ++e) load_e(min(1, ntk - 1), s1, e);
+#pragma unroll
+        for (int e = 0; e < NE; ++e) store_e(0, s0, e);
+        __syncthreads();
+        int kt = 0;
+        for (; kt + 1 < ntk; kt += 2) {
+            tile(0, s1, true, s0, min(kt + 2, ntk - 1));
+            __syncthreads();
+            tile(1, s0, kt + 2 < ntk, s1, min(kt + 3, ntk - 1));
+            __syncthreads();
+        }
+        if (kt < ntk) {
+            tile(0, s1, false, s0, kt);
+            __syncthreads();
+        }
+    }
+
+    gemm_epilogue<BM, BN, 2, 2, RC, CS, shp::C_STRIDED>(p, acc, smem, m0, n0, split, p.splits, bz,
+                                                        bo, bi, gridDim.z,
+                                                        (int64_t)bz * gridDim.x + blockIdx.x);
+}
+
 // ---- pipelined variant: operand tiles go from global memory straight into LDS
 // (gfx950 global_load_lds_dwordx4: each lane moves 16 bytes, lane i of a wavefront writes
 // bytes 16i..16i+15 of the 1 KiB block that M0 points at), through a ring of DMA_STAGES
@@ -940,8 +1191,9 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
     int bm, bn, bk;
-    bool dma;  // the pipelined gemm_dma_kernel (BM 128, BK 16) instead of gemm_mfma_kernel
-    int pg;    // gemm_mfma_kernel global prefetch depth (0 or 1: one tile, 2: two tiles)
+    bool dma;         // the pipelined gemm_dma_kernel (BM 128, BK 16) instead of gemm_mfma_kernel
+    int pg;           // gemm_mfma_kernel global prefetch depth (0 or 1: one tile, 2: two tiles)
+    bool bl = false;  // gemm_bl_kernel (buffer-loaded) instead of gemm_mfma_kernel
 };
 
 // The pipelined kernel takes row-contiguous operands whose 16-byte chunks are aligned:
@@ -1047,6 +1299,61 @@ int dispatch_combo(hipStream_t s, const GemmParams& p, int am, int bm, int cm, T
     return fail(SHP_ERR_UNSUPPORTED, "gemm: unsupported operand mode combination");
 }
 
+// gemm_bl_kernel takes 16-byte aligned row-contiguous operands whose ranges fit a buffer
+// resource with every offset below kOobOffset, and K in whole K tiles of `bk`.
+bool bl_eligible(const GemmParams& p, int am, int bm, int cm, int bk) {
+    using namespace shp;
+    if (cm != C_STRIDED || p.K < bk || p.K % bk != 0) return false;
+    if (am == A_CONV_NHWC4) {
+        if (p.cic % bk != 0) return false;
+    } else if (am == A_KVEC) {
+        if (p.sak != 1 || p.sam % 4) return false;
+    } else {
+        return false;
+    }
+    if (bm == B_NVEC) {
+        if (p.sbn != 1 || p.sbk % 4 || p.N % 4) return false;
+    } else if (bm == B_KVEC) {
+        if (p.sbk != 1 || p.sbn % 4) return false;
+    } else {
+        return false;
+    }
+    if (p.sa_outer % 4 || p.sa_inner % 4 || p.sb_outer % 4 || p.sb_inner % 4) return false;
+    if (((uintptr_t)p.a & 15) || ((uintptr_t)p.b & 15)) return false;
+    const int64_t lim = (int64_t)1 << 29;  // floats: byte offsets stay below 2 GiB
+    return bl_a_extent(p, am) <= lim && bl_b_extent(p, bm) <= lim;
+}
+
+// K tiles (bit 0: 16, bit 1: 32, bit 2: 64) for which the problem fits gemm_bl_kernel.
+int bl_mask(const GemmParams& p, int am, int bm, int cm) {
+    return (bl_eligible(p, am, bm, cm, 16) ? 1 : 0) | (bl_eligible(p, am, bm, cm, 32) ? 2 : 0) |
+           (bl_eligible(p, am, bm, cm, 64) ? 4 : 0);
+}
+
+template <int AM, int BMD>
+void launch_bl_combo(hipStream_t s, const GemmParams& p, TileCfg t, dim3 grid) {
+    if (t.bm == 128 && t.bn == 128)
+        hipLaunchKernelGGL((gemm_bl_kernel<128, 128, 32, AM, BMD>), grid, dim3(256), 0, s, p);
+    else if (t.bm == 128)
+        hipLaunchKernelGGL((gemm_bl_kernel<128, 64, 32, AM, BMD>), grid, dim3(256), 0, s, p);
+    else if (t.bk == 64)
+        hipLaunchKernelGGL((gemm_bl_kernel<64, 64, 64, AM, BMD>), grid, dim3(256), 0, s, p);
+    else if (t.bk == 16)
+        hipLaunchKernelGGL((gemm_bl_kernel<64, 64, 16, AM, BMD>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_bl_kernel<64, 64, 32, AM, BMD>), grid, dim3(256), 0, s, p);
+}
+
+int dispatch_bl(hipStream_t s, const GemmParams& p, int am, int bm, TileCfg t, dim3 grid) {
+    using namespace shp;
+    if (am == A_KVEC && bm == B_NVEC) launch_bl_combo<A_KVEC, B_NVEC>(s, p, t, grid);
+    else if (am == A_KVEC && bm == B_KVEC) launch_bl_combo<A_KVEC, B_KVEC>(s, p, t, grid);
+    else if (am == A_CONV_NHWC4 && bm == B_NVEC) launch_bl_combo<A_CONV_NHWC4, B_NVEC>(s, p, t, grid);
+    else if (am == A_CONV_NHWC4 && bm == B_KVEC) launch_bl_combo<A_CONV_NHWC4, B_KVEC>(s, p, t, grid);
+    else return fail(SHP_ERR_UNSUPPORTED, "gemm: operand forms outside the buffer-loaded kernel");
+    return SHP_OK;
+}
+
 struct Plan {
     TileCfg t;
     int splits, kps;
@@ -1055,6 +1362,10 @@ struct Plan {
 // Workgroups resident per CU, as the compiler reports them for each variant (LDS of the
 // double-buffered tiles out of 160 KiB per CU, and the VGPR+AGPR budget).
 int occupancy(TileCfg t) {
+    if (t.bl) {
+        if (t.bm == 128) return 2;
+        return t.bk == 64 ? 2 : t.bk == 16 ? 7 : 4;
+    }
     if (t.dma) return t.bn == 128 ? 2 : 3;
     if (t.bm == 128 && t.bn == 128) return t.bk == 16 ? 4 : 2;
     if (t.bm == 128) return t.bk == 16 ? 4 : 3;
@@ -1067,6 +1378,7 @@ int occupancy(TileCfg t) {
 // and the twice higher residency of the 16-deep tile wins (K = 64..256 layers measured
 // 3-16 % faster with it).
 double tile_eff(TileCfg t, int kps) {
+    if (t.bl) return t.bk == 16 && kps > 256 ? 0.85 : 1.0;
     if (t.dma) return 1.1;
     double e = (t.bm == 128 && t.bn == 128) ? 1.0 : 0.85;
     return t.bk == 16 && kps > 256 ? e * 0.85 : e;
@@ -1077,12 +1389,15 @@ double tile_eff(TileCfg t, int kps) {
 // reduction pass.
 double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps) {
     static const double kUtil[8] = {0.4, 0.6, 0.75, 0.85, 0.9, 0.92, 0.95, 1.0};
+    // the buffer-loaded kernel keeps its own MFMA stream fed: one workgroup per CU already
+    // runs at ~80 % of the CU's rate (MI355X, 1568x512x4608 on 200 CUs)
+    static const double kUtilBl[8] = {0.8, 0.9, 0.94, 0.96, 0.97, 0.98, 0.99, 1.0};
     const double cu_rate = 256.0 * 2.4e9;  // fp32 MFMA FLOP/s per CU
     int64_t tiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * nbatch;
     int64_t wgs = tiles * splits;
     int64_t per_cu = (wgs + 255) / 256;
     int resident = (int)std::min<int64_t>(occupancy(t), per_cu);
-    double util = kUtil[std::min(resident, 8) - 1];
+    double util = (t.bl ? kUtilBl : kUtil)[std::min(resident, 8) - 1];
     double wg_flops = 2.0 * t.bm * t.bn * kps;
     double cost = per_cu * wg_flops / (cu_rate * tile_eff(t, kps) * util);
     if (splits > 1) cost += (splits + 1.0) * p.M * (double)p.N * nbatch * 4.0 / 3.0e12 + 2.0e-6;
@@ -1119,11 +1434,49 @@ bool tuned_plan(const GemmParams& p, int nbatch, int amode, bool hot, Plan* out)
     return false;
 }
 
+const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 12, 16};
+
+// The buffer-loaded kernel's plan: tile, K tile and split count by the cost model, among the
+// K tiles of `blm` (bl_mask) and the tune overrides.  False when no candidate fits.
+bool plan_bl(const GemmParams& p, int nbatch, int blm, const shp::GemmTune& tn, Plan* out) {
+    static const TileCfg kBl[] = {{128, 128, 32, false, 1, true}, {128, 64, 32, false, 1, true},
+                                  {64, 64, 64, false, 1, true},   {64, 64, 32, false, 1, true},
+                                  {64, 64, 16, false, 1, true}};
+    Plan best{kBl[3], 1, 0};
+    double best_cost = 1e30;
+    for (const TileCfg& t : kBl) {
+        const int bit = t.bk == 16 ? 1 : t.bk == 32 ? 2 : 4;
+        if (!(blm & bit)) continue;
+        const int ti = t.bm == 128 ? (t.bn == 128 ? 1 : 2) : 3;
+        if (tn.tile && tn.tile != ti) continue;
+        if (tn.bk && tn.bk != t.bk) continue;
+        const int kq = t.bk == 64 ? 64 : 32;
+        for (int s : kSplits) {
+            if (tn.splits && tn.splits != s) continue;
+            int kps = ((p.K + s - 1) / s + kq - 1) / kq * kq;
+            int real = (p.K + kps - 1) / kps;
+            if (s > 1 && (real != s || kps < 128)) continue;
+            double c = plan_cost(p, nbatch, t, s, kps);
+            if (c < best_cost * 0.97) {
+                best_cost = c;
+                best = Plan{t, s, kps};
+            }
+        }
+    }
+    if (best.kps <= 0) return false;
+    *out = best;
+    return true;
+}
+
+// `blm`: the K tiles for which the buffer-loaded kernel takes the problem (0: none).  It is
+// used wherever it applies unless the tune says otherwise (bl -1, or a dma / pg override).
 Plan plan_gemm(const GemmParams& p, int nbatch, bool hot, bool dma_ok, bool conv_a,
-               const shp::GemmTune& tn, int amode = -1) {
+               const shp::GemmTune& tn, int amode = -1, int blm = 0) {
     static const int kTiles[5][2] = {{128, 128}, {128, 64}, {64, 64}, {128, 128}, {128, 64}};
-    static const int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 12, 16};
     Plan tuned;
+    if (blm && tn.bl >= 0 && (tn.bl > 0 || (tn.dma <= 0 && !tn.pg)) &&
+        plan_bl(p, nbatch, blm, tn, &tuned))
+        return tuned;
     if (tn.table >= 0 && !tn.tile && !tn.bk && !tn.splits && !tn.dma && !tn.pg && amode >= 0 &&
         tuned_plan(p, nbatch, amode, hot, &tuned))
         return tuned;
@@ -1169,11 +1522,19 @@ size_t gemm_workspace_bytes(const GemmParams& p, int amode, int bmode, int cmode
                             const GemmTune* tune) {
     static const GemmTune kAuto;
     int nbatch = p.batch_outer * p.batch_inner;
-    Plan pl = plan_gemm(p, nbatch, combo_is_hot(amode, bmode, cmode),
-                        dma_eligible(p, amode, bmode, cmode), amode == A_CONV_NHWC4,
-                        tune ? *tune : kAuto, amode);
-    if (pl.splits <= 1) return 0;
-    return kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float);
+    const bool hot = combo_is_hot(amode, bmode, cmode);
+    const bool dma_ok = dma_eligible(p, amode, bmode, cmode);
+    const int blm = bl_mask(p, amode, bmode, cmode);
+    // the larger of the plans with and without the buffer-loaded kernel: its eligibility can
+    // depend on pointer alignment the caller of this function may not know yet
+    int splits = 1;
+    for (int b : {blm, 0}) {
+        Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tune ? *tune : kAuto,
+                            amode, b);
+        splits = std::max(splits, pl.splits);
+    }
+    if (splits <= 1) return 0;
+    return kSplitCounterBytes + (size_t)splits * nbatch * p.M * p.N * sizeof(float);
 }
 
 size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
@@ -1186,9 +1547,11 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
     int am = A_KVEC, bm = B_NVEC;
     if (k == "hlo_conv_nhwc_hwio" && n >= 14) {
         p.M = q[0] * q[7] * q[8]; p.N = q[6]; p.K = q[4] * q[5] * q[3];
+        p.cn = q[0]; p.cih = q[1]; p.ciw = q[2]; p.cic = q[3]; p.ckh = q[4]; p.ckw = q[5];
         am = A_CONV_NHWC4;
     } else if ((k == "conv2d" || k == "conv2d_nhwc") && n >= 15) {
         p.M = q[0] * q[5] * q[6]; p.N = q[4]; p.K = q[1] * q[7] * q[8];
+        p.cn = q[0]; p.cic = q[1]; p.cih = q[2]; p.ciw = q[3]; p.ckh = q[7]; p.ckw = q[8];
         am = A_CONV_NHWC4;
         bm = B_KVEC;
     } else if (k == "fully_connected" && n >= 4) {
@@ -1205,6 +1568,9 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
         return 0;
     }
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) return 0;
+    // dense row-major operands, as the model graphs pass them
+    p.sam = p.K; p.sak = 1;
+    if (bm == B_KVEC) { p.sbk = 1; p.sbn = p.K; } else { p.sbk = p.N; p.sbn = 1; }
     // the largest of the hot and generic plans, so either launch finds its partials
     return std::max(gemm_workspace_bytes(p, am, bm, C_STRIDED, tune),
                     gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED, tune));
@@ -1226,7 +1592,8 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     const bool fix_ok = cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 && (p.N & 3) == 0 &&
                         (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
                         (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual));
-    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn, amode);
+    const int blm = bl_mask(p, amode, bmode, cmode);
+    Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn, amode, blm);
     size_t need = pl.splits > 1
                       ? kSplitCounterBytes + (size_t)pl.splits * nbatch * p.M * p.N * sizeof(float)
                       : 0;
@@ -1243,10 +1610,10 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     // Two-deep prefetch for the split-K 64x64 / K-tile 32 plans of NHWC convolutions: 4-7 %
     // faster on the ResNet-50 K = 1024..2304 layers (MI355X sweeps), ~2 % slower on some
     // short single-split loops, and 3x slower on the M = 32 row-major FC (one tile row).
-    if (!t.dma && t.bm == 64 && t.bn == 64 && t.bk == 32 && pl.splits > 1 &&
+    if (!t.dma && !t.bl && t.bm == 64 && t.bn == 64 && t.bk == 32 && pl.splits > 1 &&
         amode == A_CONV_NHWC4 && combo_is_hot(amode, bmode, cmode))
         t.pg = 2;
-    if (tn.pg) t.pg = tn.pg;
+    if (tn.pg && !t.bl) t.pg = tn.pg;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
     if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
     // in-kernel split-K fixup where the tile counters fit and few splits share a tile (the last
@@ -1255,8 +1622,9 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     p.fixup = pl.splits > 1 && pl.splits <= 4 && fix_ok &&
               ntiles * nbatch <= (int64_t)(kSplitCounterBytes / sizeof(int));
     dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
-    int rc = t.dma ? launch_dma(stream, p, amode, t.bn, grid)
-                 : dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
+    int rc = t.bl    ? dispatch_bl(stream, p, amode, bmode, t, grid)
+             : t.dma ? launch_dma(stream, p, amode, t.bn, grid)
+                     : dispatch_combo(stream, p, amode, bmode, cmode, t, grid);
     if (rc) return rc;
     SHP_HIP_CHECK(hipGetLastError());
     if (p.splits > 1 && !p.fixup) {

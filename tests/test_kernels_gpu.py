@@ -458,6 +458,65 @@ def test_splitk_in_kernel_fixup(ctx, orc, gemm_workspace, splits):
         _tune(ctx, "gemm_splits", 0)
 
 
+# (n, ih, ic, k, oc, stride, split-K): padding taps with an M tail and N % 64 != 0, a strided
+# 1x1 (fixed tap, scalar channel advance), a 1x1 with an M tail, a strided 3x3 with N 132,
+# split-K with the in-kernel fixup (3) and with the reduction pass (6)
+BL_CONVS = [(2, 9, 64, 3, 20, 1, 0), (3, 14, 64, 1, 72, 2, 0), (2, 6, 128, 1, 24, 1, 0),
+            (1, 9, 64, 3, 132, 2, 0), (2, 7, 128, 3, 64, 1, 3), (2, 7, 128, 3, 64, 1, 6)]
+
+
+@pytest.mark.parametrize("tile,bk", [(1, 32), (2, 32), (3, 32), (3, 16), (3, 64)],
+                         ids=["128x128k32", "128x64k32", "64x64k32", "64x64k16", "64x64k64"])
+def test_gemm_buffer_loaded_kernel(ctx, orc, gemm_workspace, tile, bk):
+    """The buffer-loaded kernel on each of its tiles: NHWC convolutions (padding taps read as
+    zeros, strided 1x1, M and N tails, split-K both ways), a row-major product with bias and
+    GELU, a batched product, the [out][in] fully-connected and the OHWI conv2d_nhwc operands.
+    Each result is checked against the oracle and, where the double-buffered kernel has the
+    same tile and K tile, bit for bit against it with the same split: both assign the K of a
+    tile to MFMA k-pairs alike, so their sums are the same."""
+    def conv_case(n, ih, ic, k, oc, s):
+        pad = (k - 1) // 2
+        oh = (ih + 2 * pad - k) // s + 1
+        x = rnd(n, ih, ih, ic)
+        w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+        b, res = rnd(oc, scale=0.01), rnd(n * oh * oh * oc)
+        push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+        return ("hlo_conv_nhwc_hwio", x, w, push[13], push,
+                dict(bias=b, residual=res, act="relu"))
+
+    cases = [(conv_case(*c[:6]), c[6]) for c in BL_CONVS]
+    a, bm = rnd(70, 128), rnd(128, 36, scale=0.1)
+    cases.append((("hlo_dot_rank2", a, bm, 70 * 36, [70, 128, 36, 70 * 36],
+                   dict(bias=rnd(36), act="gelu_erf")), 0))
+    a, bm = rnd(3, 40, 256), rnd(3, 256, 36, scale=0.1)
+    cases.append((("hlo_dot_batched", a, bm, 3 * 40 * 36, [3, 40, 256, 36, 3 * 40 * 36], {}), 2))
+    w = np.concatenate([rnd(1000 * 2048, scale=0.05), rnd(1000)])
+    cases.append((("fully_connected", rnd(32, 2048), w, 32 * 1000, [32, 2048, 1000, 32 * 1000],
+                   {}), 0))
+    w = np.concatenate([rnd(20 * 64 * 9, scale=0.1), rnd(20)])
+    cases.append((("conv2d_nhwc", rnd(2, 9, 9, 64), w, 2 * 20 * 81,
+                   [2, 64, 9, 9, 20, 9, 9, 3, 3, 1, 1, 1, 1, 1, 2 * 20 * 81], dict(act="relu6")),
+                  0))
+    try:
+        _tune(ctx, "gemm_tile", tile)
+        _tune(ctx, "gemm_bk", bk)
+        for (name, x, w, n_out, push, kw), splits in cases:
+            _tune(ctx, "gemm_splits", splits)
+            _tune(ctx, "gemm_bl", 1)
+            y = hip(ctx, name, x, w, n_out, push, **kw)
+            r = orc.run(name, x, w, n_out, push, **kw)
+            assert_close(y, r, 1e-4, 1e-4, f"buffer-loaded {name} {push[:13]} splits {splits}")
+            if bk != 64:
+                _tune(ctx, "gemm_bl", -1)
+                _tune(ctx, "gemm_dma", -1)
+                y0 = hip(ctx, name, x, w, n_out, push, **kw)
+                _tune(ctx, "gemm_dma", 0)
+                assert np.array_equal(y, y0), (name, push[:13], splits)
+    finally:
+        for key in ("gemm_bl", "gemm_dma", "gemm_tile", "gemm_bk", "gemm_splits"):
+            _tune(ctx, key, 0)
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256
