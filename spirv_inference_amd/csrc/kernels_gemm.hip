@@ -839,6 +839,159 @@ __global__ __launch_bounds__(256) void gemm_bl_kernel(GemmParams p) {
                                                         (int64_t)bz * gridDim.x + blockIdx.x);
 }
 
+// ---- persistent small-K variant (gemm_smallk_kernel) for products with K = 64 (KT) whose
+// A is plain rows (row-major, or the NHWC input of a 1x1 stride-1 unpadded convolution) and
+// whose B is [K][N]: the 1x1 convolutions of bottleneck networks.  A tiled kernel spends
+// most of such a tile in its operand prologue and its epilogue (4-8 K steps), so here:
+// * one workgroup of 512 threads per CU owns the 32-row tiles [T*r/R, T*(r+1)/R) (T tiles in
+//   all) of one TN-column slab of C; the slab of B is transposed into LDS once ([n][k], rows
+//   padded by 4 floats);
+// * the eight wavefronts form teams of WC; team i takes tiles i, i + 8/WC, ... of the range,
+//   each wave 32 rows x 32*FN columns;
+// * a wave loads its tile's A rows straight into registers in the MFMA operand layout (lane
+//   l: row l % 32, k = 8s + 4*(l / 32) .. +3 of step s, the same k remap as gemm_bl_kernel),
+//   two tiles ahead;
+// * the epilogue stores from the accumulators (each store instruction writes two 128-byte
+//   row segments), spread over the next tile's fragment steps (two accumulator sets), so the
+//   stores drain under the MFMA stream instead of stalling it; the residual of a tile is
+//   loaded into the slots of the elements stored before it.
+// M is a multiple of 32 (the host checks it), so no tile needs row checks.  ACT: 0 no
+// activation, 1 ReLU (a template parameter, so that the epilogue is straight-line code).
+// Workgroup b sits on XCD b % 8; the slabs of one row range go to workgroups of one XCD, so
+// A is fetched from HBM once and re-read from that XCD's L2.
+template <int KT, int FN, int WC, int ACT, bool RES>
+__global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int nslab, int nrange) {
+    constexpr int KS = KT / 8;               // fragment steps (8 k each) per tile
+    constexpr int TN = 32 * FN * WC;          // slab width
+    constexpr int BST = KT + 4;               // LDS row stride of the transposed slab
+    constexpr int NTEAM = 8 / WC;
+    constexpr int NST = 16 * FN;              // output elements per lane and tile
+    constexpr int SPS = (NST + KS - 1) / KS;  // of them stored per fragment step
+    __shared__ __attribute__((aligned(16))) float Bs[TN * BST];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int b = blockIdx.x;
+    const int slab = (b >> 3) % nslab;
+    const int range = (b & 7) + 8 * (b / (8 * nslab));
+    if (range >= nrange) return;
+    const int T = p.M / 32;
+    const int t_beg = (int)((int64_t)T * range / nrange);
+    const int t_end = (int)((int64_t)T * (range + 1) / nrange);
+    const int c_slab = slab * TN;
+
+    // B slab -> LDS, transposed to [n][k]
+    for (int i = tid; i < KT * TN / 4; i += 512) {
+        const int k = i / (TN / 4), n4 = (i % (TN / 4)) * 4;
+        const float4 v = *reinterpret_cast<const float4*>(p.b + (int64_t)k * p.sbk + c_slab + n4);
+        Bs[(n4 + 0) * BST + k] = v.x;
+        Bs[(n4 + 1) * BST + k] = v.y;
+        Bs[(n4 + 2) * BST + k] = v.z;
+        Bs[(n4 + 3) * BST + k] = v.w;
+    }
+    __syncthreads();
+
+    const int team = wave / WC, wc = wave % WC;
+    const int first = t_beg + team;
+    const int n = first < t_end ? (t_end - 1 - first) / NTEAM + 1 : 0;  // tiles of this team
+    if (n == 0) return;
+    const int col0 = c_slab + wc * 32 * FN + li;  // this lane's column (fn 0)
+    float bias[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bias[fn] = p.bias ? p.bias[col0 + fn * 32] : 0.0f;
+    const char* __restrict__ Ab = reinterpret_cast<const char*>(p.a);
+    const char* __restrict__ Rb = reinterpret_cast<const char*>(p.residual);
+    char* __restrict__ Cb = reinterpret_cast<char*>(p.c);
+    const unsigned sam4 = (unsigned)p.sam * 4u, scm4 = (unsigned)p.scm * 4u;
+    const unsigned aoff0 = (unsigned)li * sam4 + 16u * lh;                    // + tile rows
+    const unsigned coff0 = (unsigned)(4 * lh) * scm4 + (unsigned)col0 * 4u;  // + tile rows
+    const unsigned bsoff = (unsigned)(col0 - c_slab) * BST + 4 * lh;
+
+    auto load_a = [&](f4v (&a)[KS], int t) __attribute__((always_inline)) {
+        const unsigned off = aoff0 + (unsigned)(t * 32) * sam4;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) a[s] = *reinterpret_cast<const f4v*>(Ab + off + 32u * s);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Output element i of a lane (i = r * FN + fn): row 8*(r/4) + r%4 (+ 4*lh), column fn*32.
+    auto eoff = [&](int t, int i) __attribute__((always_inline)) {
+        const int r = i / FN, fn = i % FN;
+        return coff0 + (unsigned)(t * 32 + 8 * (r >> 2) + (r & 3)) * scm4 + 128u * fn;
+    };
+    float res[NST];  // the residual of the tile whose results are stored next
+    auto load_res = [&](int t, int i0, int i1) __attribute__((always_inline)) {
+        if constexpr (RES) {
+#pragma unroll
+            for (int i = i0; i < i1 && i < NST; ++i)
+                res[i] = *reinterpret_cast<const float*>(Rb + eoff(t, i));
+        }
+    };
+    // Stores elements [i0, i1) of tile t from acc; with RES, refills their residual slots with
+    // tile tn's, whose results are stored next.
+    auto store_some = [&](const floatx16 (&acc)[FN], int t, int tn, int i0, int i1)
+                          __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = i0; i < i1 && i < NST; ++i) {
+            float v = acc[i % FN][i / FN] + bias[i % FN];
+            if constexpr (RES) v += res[i];
+            if constexpr (ACT == 1) v = fmaxf(v, 0.0f);
+            *reinterpret_cast<float*>(Cb + eoff(t, i)) = v;
+        }
+        load_res(tn, i0, i1);
+    };
+    // The MFMAs of tile t (operands a) into acc; when `store`, tile tp's results (prev) are
+    // stored SPS per fragment step in between, so the stores drain under the MFMA stream.
+    auto mma_tile = [&](const f4v (&a)[KS], floatx16 (&acc)[FN], const floatx16 (&prev)[FN], int t,
+                        int tp, bool store) __attribute__((always_inline)) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fn][r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            f4v bf[FN];
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+                bf[fn] = *reinterpret_cast<const f4v*>(&Bs[bsoff + fn * 32 * BST + 8 * s]);
+            if (store) store_some(prev, tp, t, s * SPS, (s + 1) * SPS);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    acc[fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][q], bf[fn][q], acc[fn], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Tiles alternate between two operand register sets (each loaded two tiles ahead, clamped
+    // to the team's last tile, so every load is unconditional) and two accumulator sets (one
+    // multiplied while the other is stored).
+    const int tlast = first + (n - 1) * NTEAM;
+    f4v a0[KS], a1[KS];
+    floatx16 c0[FN], c1[FN];
+    load_res(first, 0, NST);
+    load_a(a0, first);
+    load_a(a1, min(first + NTEAM, tlast));
+    mma_tile(a0, c0, c1, first, first, false);
+    load_a(a0, min(first + 2 * NTEAM, tlast));
+    int j = 1;
+    for (; j + 1 < n; j += 2) {
+        const int t = first + j * NTEAM;  // tile j in a1, tile j + 1 in a0
+        mma_tile(a1, c1, c0, t, t - NTEAM, true);
+        load_a(a1, min(t + 2 * NTEAM, tlast));
+        mma_tile(a0, c0, c1, t + NTEAM, t, true);
+        load_a(a0, min(t + 3 * NTEAM, tlast));
+    }
+    if (j < n) {
+        const int t = first + j * NTEAM;
+        mma_tile(a1, c1, c0, t, t - NTEAM, true);
+        store_some(c1, t, t, 0, NST);
+    } else {
+        const int t = first + (j - 1) * NTEAM;
+        store_some(c0, t, t, 0, NST);
+    }
+}
+
 // ---- pipelined variant: operand tiles go from global memory straight into LDS
 // (gfx950 global_load_lds_dwordx4: each lane moves 16 bytes, lane i of a wavefront writes
 // bytes 16i..16i+15 of the 1 KiB block that M0 points at), through a ring of DMA_STAGES
@@ -1354,6 +1507,73 @@ int dispatch_bl(hipStream_t s, const GemmParams& p, int am, int bm, TileCfg t, d
     return SHP_OK;
 }
 
+// The persistent small-K kernel's variant for a problem, 0 where it does not apply: K 64 with
+// N 64 (1) or N a multiple of 256 (2); A plain rows or the input of a 1x1 stride-1 unpadded
+// NHWC convolution, B [K][N], one batch, M a multiple of 32 with enough rows that every CU
+// gets several 32-row tiles, no activation or ReLU.  (With K 128 the tiled kernel measured
+// faster on every ResNet-50 shape, 46 against 54-74 us on 25088x512x128.)
+int smallk_variant(const GemmParams& p, int am, int bm, int cm, int nbatch) {
+    using namespace shp;
+    if (nbatch != 1 || cm != C_STRIDED || p.scn != 1 || bm != B_NVEC || p.sbn != 1) return 0;
+    if (p.act != SHP_ACT_NONE && p.act != SHP_ACT_RELU) return 0;
+    if (p.sbk % 4 || ((uintptr_t)p.a & 15) || ((uintptr_t)p.b & 15) || p.M < 16384 || p.M % 32)
+        return 0;
+    // 32-bit byte offsets of A, C and the residual rows
+    const int64_t lim = (int64_t)1 << 31;
+    const int64_t a_rows = am == A_KVEC ? p.sam : p.cic;
+    if ((int64_t)p.M * a_rows * 4 >= lim || (int64_t)p.M * p.scm * 4 >= lim) return 0;
+    if (am == A_CONV_NHWC4 || am == A_CONV_NHWC) {
+        if (p.ckh != 1 || p.ckw != 1 || p.csh != 1 || p.csw != 1 || p.cpt || p.cpl ||
+            p.cih != p.coh || p.ciw != p.cow || p.cic != p.K)
+            return 0;
+    } else if (am != A_KVEC || p.sak != 1 || p.sam % 4) {
+        return 0;
+    }
+    if (p.K == 64 && p.N == 64) return 1;
+    if (p.K == 64 && p.N % 256 == 0) return 2;
+    return 0;
+}
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int KT, int FN, int WC, bool RES>
+void launch_smallk_act(hipStream_t s, const GemmParams& p, int nslab, int nrange, dim3 grid, int act) {
+    if (act == 0)
+        hipLaunchKernelGGL((gemm_smallk_kernel<KT, FN, WC, 0, RES>), grid, dim3(512), 0, s, p, nslab, nrange);
+    else
+        hipLaunchKernelGGL((gemm_smallk_kernel<KT, FN, WC, 1, RES>), grid, dim3(512), 0, s, p, nslab, nrange);
+}
+
+// One workgroup per CU: nslab column slabs x nrange row ranges (a multiple of 8, so that the
+// slabs of a range share an XCD).
+int launch_smallk(hipStream_t s, GemmParams p, int am, int variant) {
+    if (am != shp::A_KVEC) p.sam = p.cic;
+    const int tn = variant == 1 ? 64 : 256;
+    const int nslab = p.N / tn;
+    const int nrange = std::max(8, device_cus() / nslab / 8 * 8);
+    const dim3 grid((unsigned)(nrange * nslab));
+    const int act = p.act == SHP_ACT_RELU ? 1 : 0;
+    const bool res = p.residual != nullptr;
+    if (variant == 1 && res) launch_smallk_act<64, 2, 1, true>(s, p, nslab, nrange, grid, act);
+    else if (variant == 1) launch_smallk_act<64, 2, 1, false>(s, p, nslab, nrange, grid, act);
+    else if (res) launch_smallk_act<64, 2, 4, true>(s, p, nslab, nrange, grid, act);
+    else launch_smallk_act<64, 2, 4, false>(s, p, nslab, nrange, grid, act);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
 struct Plan {
     TileCfg t;
     int splits, kps;
@@ -1648,6 +1868,10 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     const bool fix_ok = cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 && (p.N & 3) == 0 &&
                         (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
                         (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual));
+    if (tn.sk >= 0) {
+        const int v = smallk_variant(p, amode, bmode, cmode, nbatch);
+        if (v) return launch_smallk(stream, p, amode, v);
+    }
     const int blm = bl_mask(p, amode, bmode, cmode);
     Plan pl = plan_gemm(p, nbatch, hot, dma_ok, amode == A_CONV_NHWC4, tn, amode, bmode, blm);
     size_t need = pl.splits > 1

@@ -517,6 +517,39 @@ def test_gemm_buffer_loaded_kernel(ctx, orc, gemm_workspace, tile, bk):
             _tune(ctx, key, 0)
 
 
+@pytest.mark.parametrize("n,ih,oc,res,act", [(8, 48, 256, True, "relu"), (8, 48, 256, False, None),
+                                             (6, 56, 64, True, "relu"), (6, 56, 64, False, "relu"),
+                                             (4, 64, 512, True, None)],
+                         ids=["n256-res-relu", "n256", "n64-res-relu", "n64-relu", "n512-res"])
+def test_gemm_smallk_kernel(ctx, orc, n, ih, oc, res, act):
+    """The persistent K = 64 kernel on 1x1 NHWC convolutions (M = 16384..18816: 32-row tiles
+    that do not divide evenly over the CUs' row ranges; N 64, one 256-column slab, two slabs),
+    with and without the residual and the ReLU.  Checked against the oracle, run twice (bit
+    for bit the same), and against the planner's kernel with the persistent one switched off:
+    both agree with the oracle, and some outputs differ in the last bits because the two pair
+    the K terms differently, which shows that the persistent kernel ran."""
+    ic = 64
+    x = rnd(n, ih, ih, ic)
+    w = rnd(1, 1, ic, oc, scale=float(np.sqrt(2.0 / ic)))
+    kw = dict(bias=rnd(oc, scale=0.01))
+    if res:
+        kw["residual"] = rnd(n * ih * ih * oc)
+    if act:
+        kw["act"] = act
+    push = [n, ih, ih, ic, 1, 1, oc, ih, ih, 1, 1, 0, 0, n * ih * ih * oc]
+    r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    assert_close(y, r, 1e-4, 1e-4, f"small-K conv {push[:7]}")
+    assert np.array_equal(y, hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, **kw))
+    try:
+        _tune(ctx, "gemm_sk", -1)
+        y0 = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    finally:
+        _tune(ctx, "gemm_sk", 0)
+    assert_close(y0, r, 1e-4, 1e-4, f"tiled conv {push[:7]}")
+    assert not np.array_equal(y, y0), "the persistent small-K kernel did not run"
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256
