@@ -992,6 +992,161 @@ __global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int n
     }
 }
 
+// ---- stem variant (conv_stem_kernel): an NHWC convolution with few input channels (the 7x7
+// stride-2 3-channel ResNet stem), whose K = KH*KW*CIC is neither a multiple of 4 nor of any
+// K tile.  For one output pixel and one kernel row ky, the KW*CIC operands are contiguous in
+// the input row, so K is laid out per kernel row, each padded to GW (a multiple of 8, 21 ->
+// 24 for the stem): k = ky*GW + e, e = kx*CIC + c.  The weights of the padding slots are zero
+// in LDS, and padding taps and slots read zero (an offset past the input's range), so the
+// products are exact.
+// * One workgroup of 512 threads per CU owns the 32-row tiles [T*r/R, T*(r+1)/R) of a
+//   64-column slab; every wavefront works alone on tiles w, w + 8, ... (32 rows x 64 columns).
+// * A lane holds row l % 32 of its tile and, per fragment step s, k = 8s + 4*(l / 32) .. +3
+//   (the k remap of gemm_bl_kernel), as four dword buffer loads; the validity of each k
+//   (kernel row inside the image, column inside the image, slot < KW*CIC) comes from two
+//   per-lane bit masks computed once per tile.  The operand of step s is reloaded with the
+//   next tile's right after the step's MFMAs, so it has a tile's MFMA time to arrive.
+// * The epilogue (bias, optional ReLU) stores tile t's results during tile t+1's steps.
+// ACT: 0 none, 1 ReLU.  M is a multiple of 32 (the host checks it).
+template <int KH, int KW, int CIC, int ACT>
+__global__ __launch_bounds__(512, 1) void conv_stem_kernel(GemmParams p, int nslab, int nrange) {
+    constexpr int GW = (KW * CIC + 7) / 8 * 8;  // padded operands per kernel row
+    constexpr int GS = GW / 8;                  // fragment steps per kernel row
+    constexpr int KS = KH * GS;                 // fragment steps per tile
+    constexpr int KT = KH * GW;
+    constexpr int BST = KT + 4;
+    constexpr int TN = 64, FN = 2;
+    constexpr int NST = 16 * FN;
+    constexpr int SPS = (NST + KS - 1) / KS;
+    static_assert(GW <= 32 && GW - 4 <= 28, "row masks are 32-bit");
+    __shared__ __attribute__((aligned(16))) float Bs[TN * BST];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int b = blockIdx.x;
+    const int slab = (b >> 3) % nslab;
+    const int range = (b & 7) + 8 * (b / (8 * nslab));
+    if (range >= nrange) return;
+    const int T = p.M / 32;
+    const int t_beg = (int)((int64_t)T * range / nrange);
+    const int t_end = (int)((int64_t)T * (range + 1) / nrange);
+    const int c_slab = slab * TN;
+
+    // weight slab -> LDS as [n][ky*GW + e], zero in the padding slots
+    for (int i = tid; i < TN * KT; i += 512) {
+        const int n = i % TN, kk = i / TN;
+        const int g = kk / GW, e = kk % GW;
+        Bs[n * BST + kk] =
+            e < KW * CIC ? p.b[(int64_t)(g * KW * CIC + e) * p.sbk + c_slab + n] : 0.0f;
+    }
+    __syncthreads();
+
+    const int first = t_beg + wave;
+    const int n = first < t_end ? (t_end - 1 - first) / 8 + 1 : 0;  // tiles of this wave
+    if (n == 0) return;
+    const int col0 = c_slab + li;
+    float bias[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) bias[fn] = p.bias ? p.bias[col0 + fn * 32] : 0.0f;
+    char* __restrict__ Cb = reinterpret_cast<char*>(p.c);
+    const unsigned scm4 = (unsigned)p.scm * 4u;
+    const unsigned coff0 = (unsigned)(4 * lh) * scm4 + (unsigned)col0 * 4u;
+    const unsigned bsoff = (unsigned)li * BST + 4 * lh;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, (int64_t)p.cn * p.cih * p.ciw * CIC);
+    const int row_elems = p.ciw * CIC;
+
+    // Tile geometry of this lane's row: element offset of (ky 0, slot 4*lh), and bit masks of
+    // the kernel rows inside the image and of the slots e' (e = e' + 4*lh) that are real
+    // operands inside the image.
+    struct Geo { int base; unsigned rowm, colm; };
+    auto geo = [&](int t) __attribute__((always_inline)) {
+        const int m = t * 32 + li;
+        const int ox = m % p.cow, q = m / p.cow, oy = q % p.coh, img = q / p.coh;
+        const int iy0 = oy * p.csh - p.cpt, ix0 = ox * p.csw - p.cpl;
+        Geo g;
+        g.base = ((img * p.cih + iy0) * p.ciw + ix0) * CIC + 4 * lh;
+        g.rowm = 0;
+#pragma unroll
+        for (int ky = 0; ky < KH; ++ky) g.rowm |= ((unsigned)(iy0 + ky) < (unsigned)p.cih ? 1u : 0u) << ky;
+        unsigned cm = 0;
+#pragma unroll
+        for (int e = 0; e < KW * CIC; ++e)
+            cm |= ((unsigned)(ix0 + e / CIC) < (unsigned)p.ciw ? 1u : 0u) << e;
+        g.colm = cm >> (4 * lh);
+        return g;
+    };
+    auto load_step = [&](f4v& a, const Geo& g, int s) __attribute__((always_inline)) {
+        const int ky = s / GS;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 8 * (s % GS) + q;  // slot of lanes 0-31; lanes 32-63 take e + 4
+            const bool ok = ((g.rowm >> ky) & (g.colm >> e) & 1u) != 0;
+            const int off = g.base + ky * row_elems + e;
+            a[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 ra, ok ? (unsigned)off * 4u : kOobOffset, 0u, 0));
+        }
+    };
+    auto eoff = [&](int t, int i) __attribute__((always_inline)) {
+        const int r = i / FN, fn = i % FN;
+        return coff0 + (unsigned)(t * 32 + 8 * (r >> 2) + (r & 3)) * scm4 + 128u * fn;
+    };
+    auto store_some = [&](const floatx16 (&acc)[FN], int t, int i0, int i1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = i0; i < i1 && i < NST; ++i) {
+            float v = acc[i % FN][i / FN] + bias[i % FN];
+            if constexpr (ACT == 1) v = fmaxf(v, 0.0f);
+            *reinterpret_cast<float*>(Cb + eoff(t, i)) = v;
+        }
+    };
+    // Tile t from a (reloaded step by step with tile tn, geometry gn) into acc; when `store`,
+    // tile tp's results (prev) are stored SPS per step.
+    f4v a[KS];
+    auto mma_tile = [&](floatx16 (&acc)[FN], const floatx16 (&prev)[FN], int tp, bool store,
+                        const Geo& gn) __attribute__((always_inline)) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fn][r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            f4v bf[FN];
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+                bf[fn] = *reinterpret_cast<const f4v*>(&Bs[bsoff + fn * 32 * BST + 8 * s]);
+            if (store) store_some(prev, tp, s * SPS, (s + 1) * SPS);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn)
+                    acc[fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][q], bf[fn][q], acc[fn], 0, 0, 0);
+            load_step(a[s], gn, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    const int tlast = first + (n - 1) * 8;
+    floatx16 c0[FN], c1[FN];
+    {
+        const Geo g0 = geo(first);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) load_step(a[s], g0, s);
+    }
+    mma_tile(c0, c1, 0, false, geo(min(first + 8, tlast)));
+    int j = 1;
+    for (; j + 1 < n; j += 2) {
+        const int t = first + j * 8;  // tile j into c1, tile j + 1 into c0
+        mma_tile(c1, c0, t - 8, true, geo(t + 8));
+        mma_tile(c0, c1, t, true, geo(min(t + 16, tlast)));
+    }
+    if (j < n) {
+        const int t = first + j * 8;
+        mma_tile(c1, c0, t - 8, true, geo(t));
+        store_some(c1, t, 0, NST);
+    } else {
+        store_some(c0, first + (j - 1) * 8, 0, NST);
+    }
+}
+
 // ---- pipelined variant: operand tiles go from global memory straight into LDS
 // (gfx950 global_load_lds_dwordx4: each lane moves 16 bytes, lane i of a wavefront writes
 // bytes 16i..16i+15 of the 1 KiB block that M0 points at), through a ring of DMA_STAGES
@@ -1574,6 +1729,30 @@ int launch_smallk(hipStream_t s, GemmParams p, int am, int variant) {
     return SHP_OK;
 }
 
+// The stem kernel takes the 7x7 3-channel NHWC convolution (any stride and padding) with N a
+// multiple of 64, M a multiple of 32 and large, no residual, no activation or ReLU.
+bool stem_eligible(const GemmParams& p, int am, int bm, int cm, int nbatch) {
+    using namespace shp;
+    if (am != A_CONV_NHWC || p.cic != 3 || p.ckh != 7 || p.ckw != 7 || p.K != 147) return false;
+    if (nbatch != 1 || cm != C_STRIDED || p.scn != 1 || bm != B_NVEC || p.sbn != 1) return false;
+    if (p.residual || (p.act != SHP_ACT_NONE && p.act != SHP_ACT_RELU)) return false;
+    if (p.N % 64 || p.M % 32 || p.M < 16384) return false;
+    const int64_t lim = (int64_t)1 << 31;
+    return (int64_t)p.cn * p.cih * p.ciw * p.cic * 4 < lim && (int64_t)p.M * p.scm * 4 < lim;
+}
+
+int launch_stem(hipStream_t s, const GemmParams& p) {
+    const int nslab = p.N / 64;
+    const int nrange = std::max(8, device_cus() / nslab / 8 * 8);
+    const dim3 grid((unsigned)(nrange * nslab));
+    if (p.act == SHP_ACT_RELU)
+        hipLaunchKernelGGL((conv_stem_kernel<7, 7, 3, 1>), grid, dim3(512), 0, s, p, nslab, nrange);
+    else
+        hipLaunchKernelGGL((conv_stem_kernel<7, 7, 3, 0>), grid, dim3(512), 0, s, p, nslab, nrange);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
 struct Plan {
     TileCfg t;
     int splits, kps;
@@ -1868,6 +2047,7 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
     const bool fix_ok = cmode == C_STRIDED && p.scn == 1 && (p.scm & 3) == 0 && (p.N & 3) == 0 &&
                         (p.sc_outer & 3) == 0 && (p.sc_inner & 3) == 0 && a16(p.c) &&
                         (!p.bias || a16(p.bias)) && (!p.residual || a16(p.residual));
+    if (tn.stem >= 0 && stem_eligible(p, amode, bmode, cmode, nbatch)) return launch_stem(stream, p);
     if (tn.sk >= 0) {
         const int v = smallk_variant(p, amode, bmode, cmode, nbatch);
         if (v) return launch_smallk(stream, p, amode, v);

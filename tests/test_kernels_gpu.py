@@ -550,6 +550,36 @@ def test_gemm_smallk_kernel(ctx, orc, n, ih, oc, res, act):
     assert not np.array_equal(y, y0), "the persistent small-K kernel did not run"
 
 
+@pytest.mark.parametrize("n,ih,oc,act", [(2, 224, 64, "relu"), (8, 96, 128, None),
+                                         (32, 113, 64, "relu")],
+                         ids=["resnet-stem", "two-slabs", "odd-width"])
+def test_conv_stem_kernel(ctx, orc, n, ih, oc, act):
+    """The 7x7 stride-2 3-channel convolution kernel (kernel rows padded to 24 operands,
+    padding taps read as zeros): the ResNet stem shape, two 64-column slabs, and an odd image
+    width (the window overhangs the right border on every output row).  Checked against the
+    oracle and against the planner's kernel with the stem kernel switched off (both agree with
+    the oracle; some outputs differ in the last bits because the two order K differently, which
+    shows that the stem kernel ran)."""
+    ic, k, s, pad = 3, 7, 2, 3
+    oh = (ih + 2 * pad - k) // s + 1
+    x = rnd(n, ih, ih, ic)
+    w = rnd(k, k, ic, oc, scale=float(np.sqrt(2.0 / (k * k * ic))))
+    kw = dict(bias=rnd(oc, scale=0.01))
+    if act:
+        kw["act"] = act
+    push = [n, ih, ih, ic, k, k, oc, oh, oh, s, s, pad, pad, n * oh * oh * oc]
+    r = orc.run("hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    y = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    assert_close(y, r, 1e-4, 1e-4, f"stem conv {push[:13]}")
+    try:
+        _tune(ctx, "gemm_stem", -1)
+        y0 = hip(ctx, "hlo_conv_nhwc_hwio", x, w, push[13], push, **kw)
+    finally:
+        _tune(ctx, "gemm_stem", 0)
+    assert_close(y0, r, 1e-4, 1e-4, f"tiled conv {push[:13]}")
+    assert not np.array_equal(y, y0), "the stem kernel did not run"
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256
