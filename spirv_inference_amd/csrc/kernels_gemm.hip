@@ -849,8 +849,8 @@ __global__ __launch_bounds__(256) void gemm_bl_kernel(GemmParams p) {
 // * the eight wavefronts form teams of WC; team i takes tiles i, i + 8/WC, ... of the range,
 //   each wave 32 rows x 32*FN columns;
 // * a wave loads its tile's A rows straight into registers in the MFMA operand layout (lane
-//   l: row l % 32, k = 8s + 4*(l / 32) .. +3 of step s, the same k remap as gemm_bl_kernel),
-//   two tiles ahead;
+//   l: row l % 32, k = 8s + 4*(l / 32) .. +3 of step s, the same k remap as gemm_bl_kernel);
+//   the operand of step s is reloaded with the next tile's right after the step's MFMAs;
 // * the epilogue stores from the accumulators (each store instruction writes two 128-byte
 //   row segments), spread over the next tile's fragment steps (two accumulator sets), so the
 //   stores drain under the MFMA stream instead of stalling it; the residual of a tile is
@@ -880,9 +880,10 @@ __global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int n
     const int t_end = (int)((int64_t)T * (range + 1) / nrange);
     const int c_slab = slab * TN;
 
-    // B slab -> LDS, transposed to [n][k]
+    // B slab -> LDS, transposed to [n][k]; consecutive lanes take consecutive k, so the LDS
+    // stores are free of bank conflicts (the reads of the small slab hit L2)
     for (int i = tid; i < KT * TN / 4; i += 512) {
-        const int k = i / (TN / 4), n4 = (i % (TN / 4)) * 4;
+        const int k = i % KT, n4 = (i / KT) * 4;
         const float4 v = *reinterpret_cast<const float4*>(p.b + (int64_t)k * p.sbk + c_slab + n4);
         Bs[(n4 + 0) * BST + k] = v.x;
         Bs[(n4 + 1) * BST + k] = v.y;
@@ -907,11 +908,8 @@ __global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int n
     const unsigned coff0 = (unsigned)(4 * lh) * scm4 + (unsigned)col0 * 4u;  // + tile rows
     const unsigned bsoff = (unsigned)(col0 - c_slab) * BST + 4 * lh;
 
-    auto load_a = [&](f4v (&a)[KS], int t) __attribute__((always_inline)) {
-        const unsigned off = aoff0 + (unsigned)(t * 32) * sam4;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) a[s] = *reinterpret_cast<const f4v*>(Ab + off + 32u * s);
-        __builtin_amdgcn_sched_barrier(0);
+    auto load_a = [&](f4v& a, int t, int s) __attribute__((always_inline)) {
+        a = *reinterpret_cast<const f4v*>(Ab + aoff0 + (unsigned)(t * 32) * sam4 + 32u * s);
     };
     // Output element i of a lane (i = r * FN + fn): row 8*(r/4) + r%4 (+ 4*lh), column fn*32.
     auto eoff = [&](int t, int i) __attribute__((always_inline)) {
@@ -939,10 +937,13 @@ __global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int n
         }
         load_res(tn, i0, i1);
     };
-    // The MFMAs of tile t (operands a) into acc; when `store`, tile tp's results (prev) are
-    // stored SPS per fragment step in between, so the stores drain under the MFMA stream.
-    auto mma_tile = [&](const f4v (&a)[KS], floatx16 (&acc)[FN], const floatx16 (&prev)[FN], int t,
-                        int tp, bool store) __attribute__((always_inline)) {
+    // The MFMAs of tile t into acc, the A operand of step s replaced by tile ta's right after
+    // the step's MFMAs (so it has a tile's MFMA time to arrive); when `store`, tile tp's
+    // results (prev) are stored SPS per fragment step in between, so the stores drain under
+    // the MFMA stream.
+    f4v a[KS];
+    auto mma_tile = [&](floatx16 (&acc)[FN], const floatx16 (&prev)[FN], int t, int tp, bool store,
+                        int ta) __attribute__((always_inline)) {
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
@@ -959,32 +960,28 @@ __global__ __launch_bounds__(512, 1) void gemm_smallk_kernel(GemmParams p, int n
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn)
                     acc[fn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][q], bf[fn][q], acc[fn], 0, 0, 0);
+            load_a(a[s], ta, s);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Tiles alternate between two operand register sets (each loaded two tiles ahead, clamped
-    // to the team's last tile, so every load is unconditional) and two accumulator sets (one
-    // multiplied while the other is stored).
+    // Tiles alternate between two accumulator sets (one multiplied while the other is
+    // stored); every operand load is unconditional (past the team's last tile it re-reads it).
     const int tlast = first + (n - 1) * NTEAM;
-    f4v a0[KS], a1[KS];
     floatx16 c0[FN], c1[FN];
     load_res(first, 0, NST);
-    load_a(a0, first);
-    load_a(a1, min(first + NTEAM, tlast));
-    mma_tile(a0, c0, c1, first, first, false);
-    load_a(a0, min(first + 2 * NTEAM, tlast));
+#pragma unroll
+    for (int s = 0; s < KS; ++s) load_a(a[s], first, s);
+    mma_tile(c0, c1, first, first, false, min(first + NTEAM, tlast));
     int j = 1;
     for (; j + 1 < n; j += 2) {
-        const int t = first + j * NTEAM;  // tile j in a1, tile j + 1 in a0
-        mma_tile(a1, c1, c0, t, t - NTEAM, true);
-        load_a(a1, min(t + 2 * NTEAM, tlast));
-        mma_tile(a0, c0, c1, t + NTEAM, t, true);
-        load_a(a0, min(t + 3 * NTEAM, tlast));
+        const int t = first + j * NTEAM;  // tile j into c1, tile j + 1 into c0
+        mma_tile(c1, c0, t, t - NTEAM, true, t + NTEAM);
+        mma_tile(c0, c1, t + NTEAM, t, true, min(t + 2 * NTEAM, tlast));
     }
     if (j < n) {
         const int t = first + j * NTEAM;
-        mma_tile(a1, c1, c0, t, t - NTEAM, true);
+        mma_tile(c1, c0, t, t - NTEAM, true, t);
         store_some(c1, t, t, 0, NST);
     } else {
         const int t = first + (j - 1) * NTEAM;
@@ -1032,9 +1029,10 @@ __global__ __launch_bounds__(512, 1) void conv_stem_kernel(GemmParams p, int nsl
     const int t_end = (int)((int64_t)T * (range + 1) / nrange);
     const int c_slab = slab * TN;
 
-    // weight slab -> LDS as [n][ky*GW + e], zero in the padding slots
+    // weight slab -> LDS as [n][ky*GW + e], zero in the padding slots; consecutive lanes take
+    // consecutive k, so the LDS stores are free of bank conflicts
     for (int i = tid; i < TN * KT; i += 512) {
-        const int n = i % TN, kk = i / TN;
+        const int kk = i % KT, n = i / KT;
         const int g = kk / GW, e = kk % GW;
         Bs[n * BST + kk] =
             e < KW * CIC ? p.b[(int64_t)(g * KW * CIC + e) * p.sbk + c_slab + n] : 0.0f;
@@ -1665,8 +1663,8 @@ int dispatch_bl(hipStream_t s, const GemmParams& p, int am, int bm, TileCfg t, d
 // The persistent small-K kernel's variant for a problem, 0 where it does not apply: K 64 with
 // N 64 (1) or N a multiple of 256 (2); A plain rows or the input of a 1x1 stride-1 unpadded
 // NHWC convolution, B [K][N], one batch, M a multiple of 32 with enough rows that every CU
-// gets several 32-row tiles, no activation or ReLU.  (With K 128 the tiled kernel measured
-// faster on every ResNet-50 shape, 46 against 54-74 us on 25088x512x128.)
+// gets several 32-row tiles, no activation or ReLU.  (With K 128 the tiled kernel is as fast
+// on the ResNet-50 shape: 45.0 against 44.9-47.2 us on 25088x512x128.)
 int smallk_variant(const GemmParams& p, int am, int bm, int cm, int nbatch) {
     using namespace shp;
     if (nbatch != 1 || cm != C_STRIDED || p.scn != 1 || bm != B_NVEC || p.sbn != 1) return 0;
