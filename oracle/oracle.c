@@ -510,6 +510,53 @@ static int k_transpose(const float* in, float* out, const int32_t* q, size_t n_o
     return 0;
 }
 
+/* ---- fused attention: the scores dot_general, the row softmax and the context dot_general
+ * of one encoder layer (bert_base.stablehlo.txt:28-49), in their arithmetic and order:
+ * scores[t] = sum_d Q[s][d] K[t][d] (d ascending), v = scores * scale + mask[t], the softmax of
+ * softmax_rows, ctx[d] = sum_t P[t] V[t][d] (t ascending); float throughout.  Q, K and V of
+ * head h are the columns q_off/k_off/v_off + h*HD of rows of ld_in floats (one fused QKV
+ * activation); ctx row (b, s) holds head h at columns h*HD of ld_out floats. */
+static void attention_fused(const float* in, const float* mask, float* out, int B, int H, int S,
+                            int HD, int64_t ld_in, int q_off, int k_off, int v_off, int64_t ld_out,
+                            float scale) {
+#pragma omp parallel
+    {
+        float* p = (float*)malloc(sizeof(float) * (size_t)S);
+        float* acc = (float*)malloc(sizeof(float) * (size_t)HD);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < (int64_t)B * H * S; ++r) {
+            const int s = (int)(r % S), h = (int)((r / S) % H), b = (int)(r / ((int64_t)S * H));
+            const float* rows = in + (int64_t)b * S * ld_in + (int64_t)h * HD;
+            const float* q = rows + (int64_t)s * ld_in + q_off;
+            float m = -INFINITY;
+            for (int t = 0; t < S; ++t) {
+                const float* k = rows + (int64_t)t * ld_in + k_off;
+                float sc = 0.0f;
+                for (int d = 0; d < HD; ++d) sc = sc + q[d] * k[d];
+                p[t] = sc;
+                float v = sc * scale + (mask ? mask[t] : 0.0f);
+                m = fmaxf(m, v);
+            }
+            float sum = 0.0f;
+            for (int t = 0; t < S; ++t) {
+                float v = p[t] * scale + (mask ? mask[t] : 0.0f);
+                p[t] = expf(v - m);
+                sum = sum + p[t];
+            }
+            for (int t = 0; t < S; ++t) p[t] = p[t] / sum;
+            for (int d = 0; d < HD; ++d) acc[d] = 0.0f;
+            for (int t = 0; t < S; ++t) {
+                const float* v = rows + (int64_t)t * ld_in + v_off;
+                for (int d = 0; d < HD; ++d) acc[d] = acc[d] + p[t] * v[d];
+            }
+            float* o = out + ((int64_t)b * S + s) * ld_out + (int64_t)h * HD;
+            for (int d = 0; d < HD; ++d) o[d] = acc[d];
+        }
+        free(p);
+        free(acc);
+    }
+}
+
 /* ---- row normalisations / softmax as the HLO op chains ------------------------------- */
 /* softmax over each row of (x*scale + mask): reduce(max) -> subtract -> exponential ->
  * reduce(sum) -> divide (bert_base.stablehlo.txt:33-49, resnet50.stablehlo.txt:1714) */
@@ -667,7 +714,7 @@ static const char* kNames[] = {
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
     "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
     "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
-    "hlo_reduce", "hlo_strided_copy"};
+    "hlo_reduce", "hlo_strided_copy", "attention_fused"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -889,6 +936,18 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
         TOTAL((int64_t)q[0] * q[1] * q[2] * q[3]);
         dot_strided(q[0], q[1], q[2], q[3], q[4], in0, q[5], q[6], q[7], q[8], in1, q[9], q[10],
                     q[11], q[12], out, q[13], q[14], q[15], q[16], bias, residual, act, alpha);
+        return 0;
+    }
+    if (!strcmp(name, "attention_fused")) {
+        /* {B, H, S, HD, ld_in, q_off, k_off, v_off, ld_out, scale_bits, total = B*S*ld_out} */
+        NEED(11);
+        const int32_t* q = push;
+        if (q[0] <= 0 || q[1] <= 0 || q[2] <= 0 || q[3] <= 0)
+            return orc_fail(-4, "attention_fused: dims");
+        TOTAL((int64_t)q[0] * q[2] * q[8]);
+        if (q[10] != (int32_t)n_out) return orc_fail(-4, "attention_fused: total");
+        attention_fused(in0, in1, out, q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8],
+                        bits_to_f32(q[9]));
         return 0;
     }
     if (!strcmp(name, "resize_bilinear")) {

@@ -2299,6 +2299,173 @@ int launch_dot_rank2(const shp::Launch& l) {
 // dot_general_strided (native): any dot_general with one contracting dim, read in place.
 // push {batch_outer, batch_inner, M, N, K, sa_outer, sa_inner, sam, sak, sb_outer,
 //       sb_inner, sbk, sbn, sc_outer, sc_inner, scm, scn}  (element strides)
+// ---- attention_fused (native): one encoder layer's attention in one launch, ctx[b, s, h, :] =
+// softmax_t(Q[b, s, h, :] . K[b, t, h, :] * scale + mask[t]) . V[b, t, h, :], the math of the
+// scores dot_general, the row softmax and the context dot_general it replaces
+// (bert_base.stablehlo.txt:28-49).  Q, K and V are read in place from the fused QKV activation.
+//
+// Sequence 128, head dim 64.  A workgroup takes 64 queries of one (batch, head); its four
+// wavefronts are 2 query halves x 2 key halves, each 32 queries x 64 keys:
+// * K and V of the head are staged in LDS as [key][d] rows padded by 4 floats (coalesced 16-byte
+//   copies); Q fragments come straight from memory;
+// * scores by fp32 MFMA (k remap of gemm_bl_kernel: lanes 32-63 take d + 4 of each step), then
+//   scale + mask, the row maximum over the wave's 64 keys by lane shuffles, the common maximum
+//   of the two key halves through LDS, exp, and the row sums;
+// * P goes through LDS into the MFMA operand layout and P.V is accumulated per key half; the
+//   key-half-1 wave hands its partial output and sum to its partner, which adds, divides and
+//   stores (two 128-byte row segments per store).
+// The arithmetic differs from the three-op chain only in the order of the sums (the divide
+// comes after P.V); the result agrees with it to fp32 rounding.
+constexpr int kAttS = 128, kAttHD = 64, kAttQB = 2;  // query blocks of 64 per (batch, head)
+
+__global__ __launch_bounds__(256) void attention_fused_kernel(const float* __restrict__ qkv,
+                                                              const float* __restrict__ mask,
+                                                              float* __restrict__ out, int H,
+                                                              int ld_in, int q_off, int k_off,
+                                                              int v_off, int ld_out, float scale) {
+    constexpr int S = kAttS, HD = kAttHD, KST = HD + 4, PST = 64 + 4;
+    __shared__ __attribute__((aligned(16))) float Ks[S * KST];       // [key][d]
+    __shared__ __attribute__((aligned(16))) float Vs[S * KST];       // [key][d]
+    __shared__ __attribute__((aligned(16))) float Ps[4][32 * PST];   // per wave: P, then O
+    __shared__ float red[4][2][32];                                  // per wave: row max, sum
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const int wq = wave >> 1, wk = wave & 1;
+    const int bh = blockIdx.x / kAttQB, qb = blockIdx.x % kAttQB;
+    const int b = bh / H, h = bh % H;
+    const float* __restrict__ base = qkv + (int64_t)b * S * ld_in + h * HD;
+
+    for (int i = tid; i < S * HD / 4; i += 256) {
+        const int key = i >> 4, d4 = (i & 15) * 4;
+        const float* row = base + (int64_t)key * ld_in;
+        *reinterpret_cast<float4*>(&Ks[key * KST + d4]) = *reinterpret_cast<const float4*>(row + k_off + d4);
+        *reinterpret_cast<float4*>(&Vs[key * KST + d4]) = *reinterpret_cast<const float4*>(row + v_off + d4);
+    }
+    const int q0 = qb * 64 + wq * 32;  // this wave's first query
+    f4v qa[HD / 8];
+#pragma unroll
+    for (int s = 0; s < HD / 8; ++s)
+        qa[s] = *reinterpret_cast<const f4v*>(base + (int64_t)(q0 + li) * ld_in + q_off + 8 * s + 4 * lh);
+    const int kb = wk * 64;  // this wave's first key
+    const float mk0 = mask ? mask[kb + li] : 0.0f, mk1 = mask ? mask[kb + 32 + li] : 0.0f;
+    __syncthreads();
+
+    floatx16 sc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[j][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < HD / 8; ++s) {
+        f4v kf[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            kf[j] = *reinterpret_cast<const f4v*>(&Ks[(kb + j * 32 + li) * KST + 8 * s + 4 * lh]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                sc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[s][q], kf[j][q], sc[j], 0, 0, 0);
+    }
+    // element r of a lane: query row 8*(r/4) + 4*lh + r%4 of the wave, key kb + 32*j + li
+    float mx[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        sc[0][r] = sc[0][r] * scale + mk0;
+        sc[1][r] = sc[1][r] * scale + mk1;
+        float m = fmaxf(sc[0][r], sc[1][r]);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        mx[r] = m;
+    }
+    if (li == 0)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave][0][8 * (r >> 2) + 4 * lh + (r & 3)] = mx[r];
+    __syncthreads();
+    float sm[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float m = fmaxf(mx[r], red[wave ^ 1][0][8 * (r >> 2) + 4 * lh + (r & 3)]);
+        sc[0][r] = expf(sc[0][r] - m);
+        sc[1][r] = expf(sc[1][r] - m);
+        float t = sc[0][r] + sc[1][r];
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) t += __shfl_xor(t, o);
+        sm[r] = t;
+    }
+    float* P = Ps[wave];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) P[(8 * (r >> 2) + 4 * lh + (r & 3)) * PST + 32 * j + li] = sc[j][r];
+    floatx16 o[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {  // 8 keys per step; lanes 32-63 take keys + 4
+        const f4v pa = *reinterpret_cast<const f4v*>(&P[li * PST + 8 * s + 4 * lh]);
+        const int k0 = kb + 8 * s + 4 * lh;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[q], Vs[(k0 + q) * KST + 32 * j + li], o[j], 0, 0, 0);
+    }
+    __syncthreads();  // every wave has read its P
+    if (wk == 1) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) P[(8 * (r >> 2) + 4 * lh + (r & 3)) * PST + 32 * j + li] = o[j][r];
+        if (li == 0)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[wave][1][8 * (r >> 2) + 4 * lh + (r & 3)] = sm[r];
+    }
+    __syncthreads();
+    if (wk == 0) {
+        const float* O1 = Ps[wave ^ 1];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
+            const float inv = 1.0f / (sm[r] + red[wave ^ 1][1][row]);
+            float* orow = out + ((int64_t)b * S + q0 + row) * ld_out + h * HD;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) orow[32 * j + li] = (o[j][r] + O1[row * PST + 32 * j + li]) * inv;
+        }
+    }
+}
+
+// attention_fused push: {B, H, S, HD, ld_in, q_off, k_off, v_off, ld_out, scale_bits,
+// total = B*S*ld_out}.
+int launch_attention_fused(const shp::Launch& l) {
+    if (l.n_push < 11) return fail(SHP_ERR_PUSH, "attention_fused needs 11 push constants");
+    const int32_t* q = l.push;
+    const int B = q[0], H = q[1], S = q[2], HD = q[3], ld_in = q[4], q_off = q[5], k_off = q[6],
+              v_off = q[7], ld_out = q[8];
+    if (B <= 0 || H <= 0 || S <= 0 || HD <= 0) return fail(SHP_ERR_SHAPE, "attention_fused: dims");
+    if (S != kAttS || HD != kAttHD)
+        return fail(SHP_ERR_UNSUPPORTED, "attention_fused: sequence 128 and head dim 64 only");
+    int rc = shp::check_total(l, (int64_t)B * S * ld_out, "attention_fused");
+    if (rc) return rc;
+    if (q[10] != (int64_t)B * S * ld_out) return fail(SHP_ERR_SHAPE, "attention_fused: total");
+    const int64_t span = (int64_t)(H - 1) * HD + HD;
+    if (q_off < 0 || k_off < 0 || v_off < 0 || q_off + span > ld_in || k_off + span > ld_in ||
+        v_off + span > ld_in || ld_out < H * HD)
+        return fail(SHP_ERR_SHAPE, "attention_fused: Q/K/V columns outside the rows");
+    if ((ld_in | q_off | k_off | v_off) & 3 || !al16(l.in0))
+        return fail(SHP_ERR_SHAPE, "attention_fused: Q/K/V rows must be 16-byte aligned");
+    if ((int64_t)B * H * kAttQB > 0x7fffffff) return fail(SHP_ERR_SHAPE, "attention_fused: grid");
+    float scale;
+    memcpy(&scale, &q[9], 4);
+    hipLaunchKernelGGL(attention_fused_kernel, dim3((unsigned)(B * H * kAttQB)), dim3(256), 0, l.stream,
+                       (const float*)l.in0, (const float*)l.in1, (float*)l.out, H, ld_in, q_off,
+                       k_off, v_off, ld_out, scale);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
 int launch_dot_general(const shp::Launch& l) {
     if (l.n_push < 17) return fail(SHP_ERR_PUSH, "dot_general_strided needs 17 push constants");
     const int32_t* q = l.push;
@@ -2335,6 +2502,7 @@ KernelEntry kGemmKernels[] = {
     // native extensions
     {"conv2d_nhwc", 15, true, launch_conv2d_nhwc},
     {"dot_general_strided", 17, true, launch_dot_general},
+    {"attention_fused", 11, false, launch_attention_fused},
 };
 const int kGemmKernelCount = sizeof(kGemmKernels) / sizeof(kGemmKernels[0]);
 

@@ -366,7 +366,8 @@ int build_efficientnet_lite0(Model& m, int batch) {
 // BERT-base encoder through the HLO path: dot (hlo_dot_rank2) with bias/GELU/residual
 // epilogues, attention as two dot_generals read in place from the fused QKV activation
 // (no transposes, compiler.rs:1043-1058), row softmax with the 1/sqrt(64) scale
-// (bert_base.stablehlo.txt:28-49), LayerNorm eps 1e-12.
+// (bert_base.stablehlo.txt:28-49), LayerNorm eps 1e-12.  At sequence 128 the three attention
+// ops are one attention_fused launch (same math, Q/K/V read in place).
 int build_bert_base(Model& m, int batch, int seq) {
     const int B = batch, S = seq, D = 768, H = 12, HD = 64, F = 3072, L = 12, V = 30522;
     const int M = B * S;
@@ -410,26 +411,34 @@ int build_bert_base(Model& m, int batch, int seq) {
         int qkv = m.tensor((uint64_t)M * 3 * D);
         std::snprintf(label, sizeof label, "layer%d_qkv", l);
         m.op("hlo_dot_rank2", x, wqkv, qkv, {M, D, 3 * D, M * 3 * D}, bqkv, -1, 0, 0.0f, label);
-        int q = m.view(qkv, 0, (uint64_t)M * 3 * D);
-        int k = m.view(qkv, D, (uint64_t)M * 3 * D - D);
-        int v = m.view(qkv, 2 * D, (uint64_t)M * 3 * D - 2 * D);
-        int scores = m.tensor((uint64_t)B * H * S * S);
-        // scores[b,h,s,t] = sum_d Q[b,s,h,d] K[b,t,h,d]
-        std::snprintf(label, sizeof label, "layer%d_scores", l);
-        m.op("dot_general_strided", q, k, scores,
-             {B, H, S, S, HD, S * 3 * D, HD, 3 * D, 1, S * 3 * D, HD, 1, 3 * D, H * S * S, S * S,
-              S, 1},
-             -1, -1, 0, 0.0f, label);
-        int probs = m.tensor((uint64_t)B * H * S * S);
-        std::snprintf(label, sizeof label, "layer%d_softmax", l);
-        m.op("softmax_rows", scores, mask, probs, {B * H * S, S, f32_bits(0.125f)}, -1, -1, 0,
-             0.0f, label);
         int ctxt = m.tensor((uint64_t)M * D);
-        // ctx[b,s,h,d] = sum_t P[b,h,s,t] V[b,t,h,d]
-        std::snprintf(label, sizeof label, "layer%d_context", l);
-        m.op("dot_general_strided", probs, v, ctxt,
-             {B, H, S, HD, S, H * S * S, S * S, S, 1, S * 3 * D, HD, 3 * D, 1, S * D, HD, D, 1},
-             -1, -1, 0, 0.0f, label);
+        if (S == 128) {
+            // the other branch's three ops in one launch (the fused kernel's sequence length)
+            std::snprintf(label, sizeof label, "layer%d_attention", l);
+            m.op("attention_fused", qkv, mask, ctxt,
+                 {B, H, S, HD, 3 * D, 0, D, 2 * D, D, f32_bits(0.125f), M * D}, -1, -1, 0, 0.0f,
+                 label);
+        } else {
+            int q = m.view(qkv, 0, (uint64_t)M * 3 * D);
+            int k = m.view(qkv, D, (uint64_t)M * 3 * D - D);
+            int v = m.view(qkv, 2 * D, (uint64_t)M * 3 * D - 2 * D);
+            int scores = m.tensor((uint64_t)B * H * S * S);
+            // scores[b,h,s,t] = sum_d Q[b,s,h,d] K[b,t,h,d]
+            std::snprintf(label, sizeof label, "layer%d_scores", l);
+            m.op("dot_general_strided", q, k, scores,
+                 {B, H, S, S, HD, S * 3 * D, HD, 3 * D, 1, S * 3 * D, HD, 1, 3 * D, H * S * S, S * S,
+                  S, 1},
+                 -1, -1, 0, 0.0f, label);
+            int probs = m.tensor((uint64_t)B * H * S * S);
+            std::snprintf(label, sizeof label, "layer%d_softmax", l);
+            m.op("softmax_rows", scores, mask, probs, {B * H * S, S, f32_bits(0.125f)}, -1, -1, 0,
+                 0.0f, label);
+            // ctx[b,s,h,d] = sum_t P[b,h,s,t] V[b,t,h,d]
+            std::snprintf(label, sizeof label, "layer%d_context", l);
+            m.op("dot_general_strided", probs, v, ctxt,
+                 {B, H, S, HD, S, H * S * S, S * S, S, 1, S * 3 * D, HD, 3 * D, 1, S * D, HD, D, 1},
+                 -1, -1, 0, 0.0f, label);
+        }
         int wo = m.weight_normal((uint64_t)D * D, 0.02f);
         int bo = m.weight_const(D, 0.0f);
         int t1 = m.tensor((uint64_t)M * D);

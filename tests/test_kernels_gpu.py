@@ -580,6 +580,32 @@ def test_conv_stem_kernel(ctx, orc, n, ih, oc, act):
     assert not np.array_equal(y, y0), "the stem kernel did not run"
 
 
+@pytest.mark.parametrize("B,H,masked,pad_out", [(2, 3, True, 0), (1, 12, False, 32), (8, 12, True, 0)],
+                         ids=["b2h3-mask", "b1h12-padded-out", "bert-b8"])
+def test_attention_fused(ctx, orc, B, H, masked, pad_out):
+    """The fused attention kernel (sequence 128, head dim 64) against the oracle: Q, K and V
+    read in place from fused QKV rows, an additive key mask, context rows wider than H*64."""
+    S, HD = 128, 64
+    D = H * HD
+    qkv = rnd(B * S, 3 * D)
+    mask = rnd(S, scale=0.5) if masked else None
+    ld_out = D + pad_out
+    sb = int(np.array([0.125], np.float32).view(np.int32)[0])
+    push = [B, H, S, HD, 3 * D, 0, D, 2 * D, ld_out, sb, B * S * ld_out]
+    y, r = both(ctx, orc, "attention_fused", qkv, mask, B * S * ld_out, push)
+    cols = np.arange(B * S * ld_out) % ld_out < D  # the padding columns are not written
+    assert_close(y[cols], r[cols], 1e-4, 1e-4, f"attention_fused {push[:9]}")
+
+
+def test_attention_fused_rejects_other_sequence_lengths(ctx):
+    from spirv_inference_amd import ShpError
+    S, HD, B, H = 64, 64, 1, 2
+    qkv = rnd(B * S, 3 * H * HD)
+    with pytest.raises(ShpError, match="sequence 128"):
+        hip(ctx, "attention_fused", qkv, None, B * S * H * HD,
+            [B, H, S, HD, 3 * H * HD, 0, H * HD, 2 * H * HD, H * HD, 1065353216, B * S * H * HD])
+
+
 def test_hlo_conv_dma_by_planner(ctx, orc):
     """A shape the planner sends to the pipelined kernel on its own (K 512, 196 tiles)."""
     n, ih, ic, oc = 8, 28, 512, 256

@@ -172,6 +172,33 @@ def test_softmax_rows_without_mask(orc):
     assert_close(y, ref, 1e-6, 1e-5, "softmax_rows no mask")
 
 
+@pytest.mark.parametrize("B,H,S,HD,masked", [(2, 3, 20, 8, True), (1, 2, 128, 64, False),
+                                              (2, 1, 7, 5, True)])
+def test_attention_fused_is_the_three_op_chain(orc, B, H, S, HD, masked):
+    """attention_fused restates the scores dot_general, softmax_rows and the context
+    dot_general on the fused QKV rows: bit for bit the same as running those three oracle ops
+    (same float arithmetic and order), and within 1e-5 of a float64 softmax(QK^T s + m) V."""
+    D = H * HD
+    qkv = rnd(B * S, 3 * D)
+    mask = rnd(S, scale=0.5) if masked else None
+    sb = int(np.array([0.3], np.float32).view(np.int32)[0])
+    y = orc.run("attention_fused", qkv, mask, B * S * D, [B, H, S, HD, 3 * D, 0, D, 2 * D, D, sb, B * S * D])
+    flat = qkv.ravel()
+    sc = orc.run("dot_general_strided", flat, flat[D:], B * H * S * S,
+                 [B, H, S, S, HD, S * 3 * D, HD, 3 * D, 1, S * 3 * D, HD, 1, 3 * D, H * S * S, S * S, S, 1])
+    pr = orc.run("softmax_rows", sc, mask, B * H * S * S, [B * H * S, S, sb])
+    cx = orc.run("dot_general_strided", pr, flat[2 * D:], B * S * D,
+                 [B, H, S, HD, S, H * S * S, S * S, S, 1, S * 3 * D, HD, 3 * D, 1, S * D, HD, D, 1])
+    assert np.array_equal(y, cx)
+    t = torch.from_numpy(qkv.astype(np.float64)).reshape(B, S, 3, H, HD)
+    q, k, v = (t[:, :, i].permute(0, 2, 1, 3) for i in range(3))  # [B, H, S, HD]
+    att = q @ k.transpose(-1, -2) * float(np.float32(0.3))
+    if masked:
+        att = att + torch.from_numpy(mask.astype(np.float64))
+    ref = (torch.softmax(att, -1) @ v).permute(0, 2, 1, 3).reshape(-1).numpy()
+    assert_close(y, ref, 1e-5, 1e-5, "attention_fused vs float64")
+
+
 def test_gelu_erfc_expansion_vs_exact(orc):
     from scipy.special import erfc
     x = np.linspace(-12, 12, 4001).astype(np.float32)
