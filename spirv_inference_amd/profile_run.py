@@ -40,6 +40,8 @@ def op_work(op, elems) -> tuple[float, float]:
         flops = 2.0 * q[0] * q[1] * q[2] * q[3] * q[4]
     elif k == "fully_connected":
         flops = 2.0 * q[0] * q[1] * q[2]
+    elif k == "attention_fused":  # push {B, H, S, HD, ...}: two S x S x HD products per head
+        flops = 4.0 * q[0] * q[1] * q[2] * q[2] * q[3]
     elif k in ("depthwise_conv2d", "depthwise_conv2d_nhwc"):
         flops = 2.0 * op.out_elems * q[6] * q[7]  # push {n, c, ih, iw, oh, ow, kh, kw, ...}
     nbytes = 4.0 * (sum(ins) + op.out_elems + extra)
