@@ -254,6 +254,34 @@ def bench_config(ctx, arch: str, batch: int, seq_len: int, steps: int):
             "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4)}
 
 
+def bench_elementwise(ctx, elems: int = 64 << 20, reps: int = 20):
+    """HBM rate of the elementwise stream kernels (north star: >= 70 % of HBM for elementwise):
+    a copy (the `reshape` kernel) and an `add` over 256 MiB float tensors, timed with a hipEvent
+    pair per launch.  Bytes = every operand read once + the output written once."""
+    a, b, c = ctx.empty(elems), ctx.empty(elems), ctx.empty(elems)
+    out = {}
+    for name, nin in (("reshape", 1), ("add", 2)):
+        for _ in range(3):
+            ctx.launch(name, a, b if nin == 2 else None, c, [elems])
+        ctx.sync()
+        ctx.timing(True)
+        ctx.timing_reset()
+        for _ in range(reps):
+            ctx.launch(name, a, b if nin == 2 else None, c, [elems])
+        ctx.sync()
+        rep = ctx.timing_report()
+        ctx.timing(False)
+        sec = sum(v[0] for v in rep.values()) / reps / 1e3
+        gbs = 4.0 * elems * (nin + 1) / sec / 1e9
+        out["copy" if name == "reshape" else name] = {
+            "kernel": name, "bytes_per_launch": 4 * elems * (nin + 1), "us": round(sec * 1e6, 2),
+            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    for t in (a, b, c):
+        t.free()
+    return out
+
+
 def time_decode(ctx, lm, prompt, n_new: int):
     lm.reset()
     for t in prompt:
@@ -372,6 +400,9 @@ def main() -> int:
                     help="skip the MobileNetV2 / EfficientNet-Lite0 / BERT latency lines")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run one `reshape` copy of this many MiB (counter calibration)")
+    ap.add_argument("--elementwise-only", action="store_true",
+                    help="only the elementwise HBM measurement (the profiling entry of "
+                         "profiles/elementwise_256mib.md); prints its JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no collectives or sharding); "
@@ -381,6 +412,9 @@ def main() -> int:
     from spirv_inference_amd import Context
     ctx = Context("any")
     log(f"device {ctx.device_name}")
+    if args.elementwise_only:
+        print(json.dumps({"elementwise": bench_elementwise(ctx)}), flush=True)
+        return 0
     rn = bench_resnet(ctx, args.steps, args.warmup, args.batch, args.concurrency)
     log(f"resnet50 b{args.batch} (one chain): {rn['img_s']:.1f} img/s, "
         f"{rn['ms_per_step']:.3f} ms/step (eager+events {rn['eager_ms_per_step']:.3f} ms), "
@@ -434,6 +468,9 @@ def main() -> int:
             log(f"cpu oracle decode, 1 thread: {cpu_dec1['value']:.3f} tok/s")
         oracle.set_threads(cores)
 
+    elementwise = bench_elementwise(ctx)
+    log("elementwise: " + ", ".join(f"{k} {v['achieved']:.0f} GB/s ({100 * v['frac']:.1f} %)"
+                                   for k, v in elementwise.items()))
     traffic = measured_conv_traffic(args.batch)
     host_cpu = cpu_model()
     line = {
@@ -504,6 +541,7 @@ def main() -> int:
                 ("bert_base", "bert_base_b8_s128"))},
             "configs_hbm_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE of an eager forward per config, "
                                   "profiles/<config>.md",
+            "elementwise": elementwise,
         },
     }
     if dec is not None:

@@ -481,8 +481,9 @@ def model_bindings(model, spec):
             out.append(model.input(0))
         elif label == "embeddings_ln":
             out.append(tensor(by_label["embeddings_ln"].out, n))
-        elif label == "mask":
-            out.append(tensor(by_label["layer0_softmax"].in1, n))
+        elif label == "mask":  # the softmax's, or the fused attention's at sequence 128
+            op = by_label.get("layer0_softmax") or by_label["layer0_attention"]
+            out.append(tensor(op.in1, n))
         else:
             name, part = label.rsplit("/", 1)
             op = by_label[name]

@@ -20,7 +20,9 @@ short list of registry launches and replays it:
   epilogue activations (scheduler.rs:1146-1197's ReLU/ReLU6 and the GELU/SiLU/sigmoid/tanh
   forms).
 * Row kernels.  reduce(max) -> subtract -> exponential -> reduce(sum) -> divide over the last
-  axis (with an optional preceding scale multiply and mask add) is `softmax_rows`; the mean /
+  axis (with an optional preceding scale multiply and mask add) is `softmax_rows` (and a
+  scores dot -> softmax -> context dot over the column blocks of a fused QKV activation, at
+  sequence 128 and head dim 64, is one `attention_fused`); the mean /
   variance / rsqrt chain of a LayerNorm is `layernorm_rows`; x * rsqrt(mean(x*x) + eps) * w is
   `rmsnorm_rows`; reduce(sum over H, W) / (H*W) of an NHWC tensor is `global_avg_pool_nhwc`;
   a zero pad in front of a convolution becomes the convolution's padding.
@@ -1050,10 +1052,65 @@ class HloProgram:
             self._launch("hlo_dot_rank2", self._h(A), self._h(B), self._h(out),
                          [M, K, N, M * N], out_elems=M * N, **e)
         else:
-            self._launch("dot_general_strided", self._h(A), self._h(B), self._h(out),
-                         [bo, bi, M, N, K, sa[0], sa[1], am, ak, sb[0], sb[1], bk, bn,
-                          sc[0], sc[1], cm, cn], out_elems=bsz * M * N, **e)
+            push = [bo, bi, M, N, K, sa[0], sa[1], am, ak, sb[0], sb[1], bk, bn,
+                    sc[0], sc[1], cm, cn]
+            if not (bias or residual or act) and self._fuse_attention(A, B, out, push):
+                return out
+            self._launch("dot_general_strided", self._h(A), self._h(B), self._h(out), push,
+                         out_elems=bsz * M * N, **e)
+            self._last_dot = (len(self.launches) - 1, A, B, out, push)
         return out
+
+    def _fuse_attention(self, P: View, V: View, out: View, push: list) -> bool:
+        """The context dot of an attention block: when the two launches before it are the
+        scores dot (Q . K^T) and the row softmax that reads it, and this dot reads the softmax's
+        output, with Q, K and V column blocks of one row-major buffer (sequence 128, head dim
+        64, heads side by side, the layout of a fused QKV activation), replace the three by
+        one `attention_fused` launch (the C++ graph's op for the same block)."""
+        sm, dt = getattr(self, "_last_softmax", None), getattr(self, "_last_dot", None)
+        n = len(self.launches)
+        if sm is None or dt is None or sm[0] != n - 1 or dt[0] != n - 2:
+            return False
+        _, x, y, mask, bits = sm
+        _, Q, K, S_out, sp = dt
+        B, H, S, _, HD = sp[:5]
+        if S != 128 or HD != 64 or push[:5] != [B, H, S, HD, S]:
+            return False
+        if not (P.buf is y.buf and P.off == y.off and x.buf is S_out.buf and x.off == S_out.off):
+            return False
+        if not (Q.buf is K.buf is V.buf):
+            return False
+        ld = sp[7]  # Q row stride
+        if B == 1:  # a size-1 batch dim has no stride of its own: use the row-major one
+            sp, push = list(sp), list(push)
+            sp[5] = sp[9] = S * ld
+            sp[13], push[5], push[9] = H * S * S, H * S * S, S * ld
+            push[13] = S * push[15]
+        want_scores = [B, H, S, S, HD, S * ld, HD, ld, 1, S * ld, HD, 1, ld]
+        if sp[:13] != want_scores or sp[13:] != [H * S * S, S * S, S, 1]:
+            return False
+        if push[5:13] != [H * S * S, S * S, S, 1, S * ld, HD, ld, 1]:
+            return False
+        ld_out = push[15]
+        if push[13:] != [S * ld_out, HD, ld_out, 1] or ld_out < H * HD:
+            return False
+        base = min(Q.off, K.off, V.off)
+        offs = [Q.off - base, K.off - base, V.off - base]
+        if any(o % 4 for o in offs + [ld]) or any(o + H * HD > ld for o in offs):
+            return False
+        total = B * S * ld_out
+        self.launches = self.launches[:-2]
+        self._last_softmax = self._last_dot = None
+        self.fused_counts["softmax"] -= 1
+        if not self.fused_counts["softmax"]:
+            del self.fused_counts["softmax"]
+        span = (B * S - 1) * ld + max(offs) + H * HD  # elements the kernel reads from `base`
+        self._launch("attention_fused", self.b.sub(Q.buf.handle, base, span),
+                     self._h(mask) if mask is not None else None,
+                     self.b.sub(out.buf.handle, out.off, total),
+                     [B, H, S, HD, ld, *offs, ld_out, bits, total], out_elems=total)
+        self._note("attention")
+        return True
 
     def _out_layout(self, op: HloOp, shape: list[int]) -> View | None:
         """If the dot's only reader is a transpose (after identity transposes), a buffer in
@@ -1108,6 +1165,7 @@ class HloProgram:
                 bits = int(np.array([g["scale"]], np.float32).view(np.int32)[0])
                 self._launch("softmax_rows", self._h(x), self._h(mask) if mask else None,
                              self._h(out), [g["rows"], g["cols"], bits], out_elems=out.n)
+                self._last_softmax = (len(self.launches) - 1, x, out, mask, bits)
                 self._note("softmax")
                 return out
             if kind in ("layernorm", "rmsnorm"):

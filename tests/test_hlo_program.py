@@ -97,6 +97,25 @@ def test_fused_bert_matches_numpy_and_op_walk():
     assert_close(y, walk.reshape(y.shape), 1e-5, 1e-5, "fused vs op-by-op walk")
 
 
+def test_attention_block_fuses_at_sequence_128():
+    """At sequence 128 and head dim 64 the scores dot -> softmax -> context dot of each layer
+    compile to one attention_fused launch reading the fused QKV rows in place (the C++
+    graph's op), and the result still matches float64 numpy and the op-by-op walk."""
+    text, _ = G.bert_base(1, 128, 1, 128, 2, 256)
+    ops = X.parse_hlo_text(text)
+    params = seeded_params(ops, seed=7)
+    _, prog, (y,) = _run(text, params)
+    assert prog.fused_counts.get("attention") == 1 and "softmax" not in prog.fused_counts
+    kinds = collections.Counter(l[0] for l in prog.launches)
+    assert kinds["attention_fused"] == 1 and "dot_general_strided" not in kinds
+    push = next(l[4] for l in prog.launches if l[0] == "attention_fused")
+    assert push[:9] == [1, 2, 128, 64, 3 * 128, 0, 128, 256, 128]
+    ref = eval_numpy(ops, params)
+    assert_close(y, ref, 1e-4, 1e-4, "fused-attention BERT vs float64 numpy")
+    walk, _ = X.HloExecutor(OracleBackend(), ops).run(params)
+    assert_close(y, walk.reshape(y.shape), 1e-5, 1e-5, "fused-attention vs op-by-op walk")
+
+
 def test_fused_program_on_reference_bert_block():
     """The reference's own BERT block fixture: its erfc-expanded GELU (about 90 ops) is
     recognised as the GELU epilogue of the last dot."""
