@@ -25,7 +25,14 @@
 //
 // Weight rows are streamed with 16-byte non-temporal loads, up to three chunks (64 KB each per
 // CU) ahead of the arithmetic, on a schedule that keeps each CU's load pipe (~30 GB/s, ~64 KB
-// in flight) busy through the short latency-bound phases (see the layer loop).
+// in flight) busy through the short latency-bound phases (see the layer loop).  The
+// workgroups without an attention head also park two gate/up chunks in LDS during the
+// attention phase (five chunks resident when gate/up starts), and the gate/up rows are split
+// 1:2 between the workgroups with an attention head and the others.
+//
+// Each chunk ends in a workgroup reduction whose latency is paid once per chunk (~300 per
+// token), so every cross-lane step is a VALU operation (v_permlane32/16_swap, DPP) rather
+// than an LDS-routed shuffle.
 //
 // Cross-workgroup data (qkv, x, act, the KV cache rows, the argmax candidates) is written and
 // read with agent-scope relaxed atomics, i.e. stores and loads that go to the device-coherent
@@ -77,18 +84,9 @@ __device__ __forceinline__ float ld_coh(const float* p) {
 __device__ __forceinline__ void st_coh(float* p, float v) {
     __hip_atomic_store((SHP_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float4 ld_coh4(const float* p) {
-    SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)p;
-    unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float4(__uint_as_float((unsigned)lo), __uint_as_float((unsigned)(lo >> 32)),
-                       __uint_as_float((unsigned)hi), __uint_as_float((unsigned)(hi >> 32)));
-}
-// The same with a uniform base and a 32-bit per-lane byte offset (SGPR-base addressing).
-__device__ __forceinline__ float ld_coh_at(const float* base, unsigned byte_off) {
-    return __hip_atomic_load((SHP_GLOBAL float*)((const SHP_GLOBAL char*)base + byte_off),
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Device-coherent 16-byte load at a uniform base plus a 32-bit per-lane byte offset: the
+// address is formed from scalar registers at the load, so the compiler keeps no 64-bit per-lane
+// pointer live (such pointers get spilled, and a spill reload waits for every load in flight).
 __device__ __forceinline__ float4 ld_coh4_at(const float* base, unsigned byte_off) {
     SHP_GLOBAL unsigned long long* q =
         (SHP_GLOBAL unsigned long long*)((const SHP_GLOBAL char*)base + byte_off);
@@ -100,20 +98,51 @@ __device__ __forceinline__ float4 ld_coh4_at(const float* base, unsigned byte_of
 __device__ __forceinline__ float dot4(float4 a, float4 b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
+// Cross-lane VALU helpers (gfx950): v_permlane32_swap / v_permlane16_swap exchange halves and
+// rows of 16 lanes; DPP row rotations reach lanes within a row.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum / max over the wavefront, in every lane.  Bit for bit the xor butterfly (o = 32 .. 1):
+// after the lane-bit-5 and -4 steps every value is symmetric under those bits, and after each
+// rotation step under one more, so a row rotation by 8, 4, 2, 1 reads a lane holding the same
+// value as lane ^ 8, ^ 4, ^ 2, ^ 1.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    v += dpp<0x128>(v);  // row_ror:8
+    v += dpp<0x124>(v);  // row_ror:4
+    v += dpp<0x122>(v);  // row_ror:2
+    v += dpp<0x121>(v);  // row_ror:1
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x122>(v));
+    v = fmaxf(v, dpp<0x121>(v));
     return v;
 }
-
 __device__ __forceinline__ void part(int n, int b, int g, int& r0, int& r1) {
     r0 = (int)((int64_t)n * b / g);
     r1 = (int)((int64_t)n * (b + 1) / g);
+}
+// As part(), with workgroups b < na weighted wa and the others wb.
+__device__ __forceinline__ void part_w(int n, int b, int g, int na, int wa, int wb, int& r0,
+                                       int& r1) {
+    auto cw = [&](int i) -> int64_t {
+        return i <= na ? (int64_t)i * wa : (int64_t)na * wa + (int64_t)(i - na) * wb;
+    };
+    const int64_t tot = cw(g);
+    r0 = (int)((int64_t)n * cw(b) / tot);
+    r1 = (int)((int64_t)n * cw(b + 1) / tot);
 }
 
 // Sum over the workgroup; `scratch` holds NW floats.  Ends with a barrier so the scratch
@@ -151,31 +180,35 @@ __device__ __forceinline__ void load_chunk(float4 (&b)[NB], const float* __restr
     }
 }
 
-// Eight per-thread partial sums -> eight wavefront totals in 10 shuffles: each step halves
-// the values a lane carries while doubling the lanes summed.  Afterwards lane 8r holds the
-// total of row r.
+// Eight per-thread partial sums -> eight wavefront totals, all in VALU cross-lane operations:
+// each step halves the values a lane carries while doubling the lanes summed (lane bit 5 by
+// v_permlane32_swap, bit 4 by v_permlane16_swap, bit 3 by a DPP row rotation), then a DPP
+// shift tree sums lanes 8r .. 8r+7 into lane 8r.  Lane 8r ends with the total of row r, added
+// in the same order as an xor butterfly.
 __device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
     float a[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float keep = b5 ? v[i + 4] : v[i];
-        float send = b5 ? v[i] : v[i + 4];
-        a[i] = keep + __shfl_xor(send, 32);
+        // lanes < 32: v[i] of lanes l and l + 32; lanes >= 32: v[i + 4] of lanes l - 32 and l
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
+                                                        __float_as_uint(v[i + 4]), false, false);
+        a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
     float c[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        float keep = b4 ? a[i + 2] : a[i];
-        float send = b4 ? a[i] : a[i + 2];
-        c[i] = keep + __shfl_xor(send, 16);
+        // even rows of 16 lanes: a[i] of lanes l and l + 16; odd rows: a[i + 2]
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]),
+                                                        __float_as_uint(a[i + 2]), false, false);
+        c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    float keep = b3 ? c[1] : c[0];
-    float send = b3 ? c[0] : c[1];
-    float w = keep + __shfl_xor(send, 8);
-    w += __shfl_xor(w, 4);
-    w += __shfl_xor(w, 2);
-    w += __shfl_xor(w, 1);
+    const bool b3 = lane & 8;
+    const float keep = b3 ? c[1] : c[0];
+    const float send = b3 ? c[0] : c[1];
+    float w = keep + dpp<0x128>(send);  // row_ror:8 = lane ^ 8 within a row
+    w += dpp<0x104>(w);                 // row_shl:4: lane l += lane l + 4
+    w += dpp<0x102>(w);                 // row_shl:2
+    w += dpp<0x101>(w);                 // row_shl:1
     return w;
 }
 
@@ -305,29 +338,58 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4,
 }
 
 
-// As stream_rows, with chunks 0, 1 and 2 already issued into c0, c1 and c2.
-template <int J, int CH, int EPI>
-__device__ __forceinline__ void stream_rows3(const float* __restrict__ W, int K4, int r0, int r1,
-                                             const float4 (&xv)[J], float4 (&c0)[NB],
-                                             float4 (&c1)[NB], float4 (&c2)[NB], float* red,
-                                             int& rsel, Epi& e, const float* zero_row) {
+// LDS chunk stage: thread t keeps float4 i of a register chunk at slot[i * NT + t]
+// (consecutive threads, consecutive 16 bytes: conflict-free), and reads back only its own.
+__device__ __forceinline__ void stage_chunk(float4* slot, const float4 (&b)[NB]) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) slot[i * NT + threadIdx.x] = b[i];
+}
+template <int CH>
+__device__ __forceinline__ void chunk_dots_lds(const float4* slot, const float4 (&xv)[1],
+                                               float (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) v[i] += dot4(slot[i * NT + threadIdx.x], xv[0]);
+}
+
+// Rows [r0, r1) in chunks of CH rows, with chunks 0 .. nls-1 staged in LDS (slot c at
+// stage + c * NB * NT) and chunks nls .. nls+2 already issued into c0, c1 and c2; chunk c+3 is
+// issued into a register set as soon as the dot products of chunk c have read it.
+template <int CH, int EPI>
+__device__ __forceinline__ void stream_rows_staged(const float* __restrict__ W, int K4, int r0,
+                                                   int r1, int nls, const float4* stage,
+                                                   const float4 (&xv)[1], float4 (&c0)[NB],
+                                                   float4 (&c1)[NB], float4 (&c2)[NB],
+                                                   float* red, int& rsel, Epi& e,
+                                                   const float* zero_row) {
     const int nch = (r1 - r0 + CH - 1) / CH;
     float v[8];
-    for (int c = 0; c < nch; c += 3) {
-        chunk_dots<J, CH>(c0, xv, v);
-        load_chunk<J, CH>(c0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
+    // The resident register chunks first, so that chunk nls + 3 streams from the start.
+    for (int c = nls; c < nch; c += 3) {
+        chunk_dots<1, CH>(c0, xv, v);
+        load_chunk<1, CH>(c0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
         chunk_reduce<CH, EPI>(v, r0 + c * CH, r1, red, rsel, e);
-        stamp_in(e, 4 + c);
-        if (c + 1 >= nch) break;
-        chunk_dots<J, CH>(c1, xv, v);
-        load_chunk<J, CH>(c1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
-        stamp_in(e, 5 + c);
-        if (c + 2 >= nch) break;
-        chunk_dots<J, CH>(c2, xv, v);
-        load_chunk<J, CH>(c2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
-        stamp_in(e, 6 + c);
+        if (c + 1 < nch) {
+            chunk_dots<1, CH>(c1, xv, v);
+            load_chunk<1, CH>(c1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
+            chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
+            if (c + 2 < nch) {
+                chunk_dots<1, CH>(c2, xv, v);
+                load_chunk<1, CH>(c2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
+                chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
+            }
+        }
+        if (c == nls) {
+            for (int k = 0; k < nls; ++k) {
+                chunk_dots_lds<CH>(stage + k * NB * NT, xv, v);
+                chunk_reduce<CH, EPI>(v, r0 + k * CH, r1, red, rsel, e);
+            }
+        }
+    }
+    for (int k = 0; k < nls && k < nch && nch <= nls; ++k) {
+        chunk_dots_lds<CH>(stage + k * NB * NT, xv, v);
+        chunk_reduce<CH, EPI>(v, r0 + k * CH, r1, red, rsel, e);
     }
 }
 
@@ -387,20 +449,30 @@ __device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long lon
 // norm_load issues this thread's float4 of x (device-coherent unless it is a read-only row,
 // the embedding) and keeps it in xs (LDS) for the residual add of the next phase;
 // norm_finish forms xv = (x * rsqrt(mean(x^2) + eps)) * w.  K4 <= NT.
-__device__ __forceinline__ float4 norm_load(const float* __restrict__ x, bool coherent, int K) {
+struct NormIn {
+    float4 x, w;
+};
+__device__ __forceinline__ NormIn norm_load(const float* __restrict__ x, bool coherent, int K,
+                                            const float* __restrict__ w) {
     const int t = threadIdx.x;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (t < K / 4) v = coherent ? ld_coh4(x + 4 * t) : ldg4(x + 4 * t);
-    return v;
+    NormIn r;
+    r.x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    r.w = r.x;
+    if (t < K / 4) {
+        r.x = coherent ? ld_coh4_at(x, (unsigned)t * 16u) : ldg4(x + 4 * t);
+        r.w = ldg4(w + 4 * t);
+    }
+    return r;
 }
-__device__ __forceinline__ void norm_finish(float4 v, const float* __restrict__ w, int K, float eps,
-                                           float* scratch, float* xs, float4 (&xv)[1]) {
+__device__ __forceinline__ void norm_finish(NormIn in, int K, float eps, float* scratch,
+                                            float* xs, float4 (&xv)[1]) {
     const int t = threadIdx.x;
+    float4 v = in.x;
     if (t < K / 4) *reinterpret_cast<float4*>(xs + 4 * t) = v;
     float ss = block_sum(dot4(v, v), scratch);
     const float inv = 1.0f / sqrtf(ss / (float)K + eps);
     if (t < K / 4) {
-        float4 g = ldg4(w + 4 * t);
+        const float4 g = in.w;
         v = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z,
                         (v.w * inv) * g.w);
     }
@@ -462,14 +534,16 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
             for (int u = 0; u < 2; ++u) {
                 const int f = t + NT * u, row = f >> 4, c4 = f & 15;
                 if (row < nrows) {
-                    k4[u] = ld_coh4(kg + (int64_t)(t0 + row) * 64 + c4 * 4);
-                    v4[u] = ld_coh4(vg + (int64_t)(t0 + row) * 64 + c4 * 4);
+                    const unsigned off = (unsigned)((t0 + row) * 64 + c4 * 4) * 4u;
+                    k4[u] = ld_coh4_at(kg, off);
+                    v4[u] = ld_coh4_at(vg, off);
                 }
             }
             if (t0 == 0 && t < 48) {  // q_h, k_g, v_g: 3 x 16 float4
                 const int which = t >> 4, c4 = t & 15;
                 const int src = which == 0 ? h * 64 : which == 1 ? (nq + g) * 64 : (nq + nkv + g) * 64;
-                *reinterpret_cast<float4*>(cur + which * 64 + c4 * 4) = ld_coh4(a.qkv + src + c4 * 4);
+                *reinterpret_cast<float4*>(cur + which * 64 + c4 * 4) =
+                    ld_coh4_at(a.qkv, (unsigned)(src + c4 * 4) * 4u);
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -564,7 +638,8 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
     int qa0, qa1, h0, h1, p0, p1, v0, v1;
     part(qkv_rows, b, G, qa0, qa1);
     part(H, b, G, h0, h1);
-    part(a.ffn, b, G, p0, p1);  // gate/up pairs
+    // gate/up pairs: a workgroup with an attention head takes half of the others' share
+    part_w(a.ffn, b, G, min(a.n_heads, G), 1, 2, p0, p1);
     part(a.vocab, b, G, v0, v1);
 
     float4 b0[NB], b1[NB], b2[NB];
@@ -584,6 +659,10 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
 
 
     const bool attn_wg = b < a.n_heads;  // this workgroup computes an attention head
+    // The other workgroups stage gate/up chunks 0 and 1 in LDS (over the attention staging,
+    // which they do not use) during the attention phase.
+    const int nls = attn_wg ? 0 : 2;
+    float4* stage = reinterpret_cast<float4*>(kv_s);
     load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
     load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
     for (int it = 0; it < a.n_tokens; ++it) {
@@ -597,14 +676,15 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             // issue order, so a load issued before a barrier delays that barrier's poll.  The
             // pipe is kept busy through the short phases: qkv chunks 0-1 at the previous
             // barrier, Wo at the start of the qkv phase, gate/up 0-1 at the qkv barrier (or,
-            // for the workgroups that compute attention, after it), gate/up 2 at the Wo
-            // barrier, down 0-1 at the gate/up barrier.
+            // for the workgroups that compute attention, after it), on the others gate/up 0-1
+            // moved to LDS and 2-3 issued at the attention barrier, the next gate/up chunk at
+            // the Wo barrier, down 0-1 at the gate/up barrier.
             // ---- A: qkv (at most two chunks, both resident) -------------------------------
             {
-                float4 xr = norm_load(xin, l != 0, H);
+                NormIn xr = norm_load(xin, l != 0, H, L.attn_norm);
                 load_chunk<1, 8>(b2, L.wo, Q4, h0, h1, a.zero_row);
                 float4 xv[1];
-                norm_finish(xr, L.attn_norm, H, a.eps, scratch, xs, xv);
+                norm_finish(xr, H, a.eps, scratch, xs, xv);
                 e.out = a.qkv;
                 chunk_step<1, 8, EPI_STORE>(b0, xv, qa0, qa1, red, rsel, e);
                 chunk_step<1, 8, EPI_STORE>(b1, xv, qa0 + 8, qa1, red, rsel, e);
@@ -625,6 +705,11 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             if (attn_wg) {
                 load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
                 load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+            } else {
+                stage_chunk(stage, b0);
+                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0 + 16, 2 * p1, a.zero_row);
+                stage_chunk(stage + NB * NT, b1);
+                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 24, 2 * p1, a.zero_row);
             }
             target += 1;
             if (!bar_wait(a, target, okw)) return;
@@ -632,25 +717,25 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             // ---- B2: Wo + residual (one chunk: h1 - h0 <= 8) ------------------------------
             {
                 float4 xv[1];
-                xv[0] = t < Q4 ? ld_coh4(a.att + 4 * t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                xv[0] = t < Q4 ? ld_coh4_at(a.att, (unsigned)t * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 e.out = a.x;
                 e.resid = xs;
                 chunk_step<1, 8, EPI_RESID>(b2, xv, h0, h1, red, rsel, e);
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
-            load_chunk<1, 8>(b2, L.w_gu, H4, 2 * p0 + 16, 2 * p1, a.zero_row);
+            load_chunk<1, 8>(b2, L.w_gu, H4, 2 * p0 + 8 * (nls + 2), 2 * p1, a.zero_row);
             target += 1;
             if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- C: gate/up + SwiGLU ------------------------------------------------------
             {
-                float4 xr = norm_load(a.x, true, H);
+                NormIn xr = norm_load(a.x, true, H, L.ffn_norm);
                 float4 xv[1];
-                norm_finish(xr, L.ffn_norm, H, a.eps, scratch, xs, xv);
+                norm_finish(xr, H, a.eps, scratch, xs, xv);
                 e.out = a.act;
-                stream_rows3<1, 8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, xv, b0, b1, b2, red,
-                                               rsel, e, a.zero_row);
+                stream_rows_staged<8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, nls, stage, xv, b0,
+                                                  b1, b2, red, rsel, e, a.zero_row);
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
@@ -665,7 +750,7 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
 #pragma unroll
                 for (int jj = 0; jj < JF; ++jj) {
                     const int c = t + NT * jj;
-                    xv[jj] = c < F4 ? ld_coh4(a.act + 4 * c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    xv[jj] = c < F4 ? ld_coh4_at(a.act, (unsigned)c * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 }
                 e.out = a.x;
                 e.resid = xs;
@@ -688,9 +773,9 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
         }
         // ---- E: lm_head + per-workgroup argmax ---------------------------------------------
         {
-            float4 xr = norm_load(a.x, true, H);
+            NormIn xr = norm_load(a.x, true, H, a.final_norm);
             float4 xv[1];
-            norm_finish(xr, a.final_norm, H, a.eps, scratch, xs, xv);
+            norm_finish(xr, H, a.eps, scratch, xs, xv);
             Epi e{};
             e.out = a.logits;
             e.best = -FLT_MAX;
@@ -772,7 +857,9 @@ const void* pick_kernel(int jf) {
 
 
 size_t lds_bytes(const PersistArgs& a) {
-    size_t floats = 256 + (size_t)a.hidden + 64 * KSTRIDE + 64 * 64 + 4 * 64 + NW * 64;
+    const size_t att = 64 * KSTRIDE + 64 * 64 + 4 * 64 + NW * 64;
+    const size_t staged = 2 * NB * NT * 4;  // two gate/up chunks (float4 per thread per row)
+    size_t floats = 256 + (size_t)a.hidden + (att > staged ? att : staged);
     return floats * sizeof(float);
 }
 
