@@ -30,9 +30,13 @@
 // attention phase (five chunks resident when gate/up starts), and the gate/up rows are split
 // 1:2 between the workgroups with an attention head and the others.
 //
-// Each chunk ends in a workgroup reduction whose latency is paid once per chunk (~300 per
-// token), so every cross-lane step is a VALU operation (v_permlane32/16_swap, DPP) rather
-// than an LDS-routed shuffle.
+// GEMV layout: a chunk is 8 rows, one per wavefront, and a wavefront reads its row in 1 KB
+// contiguous loads against the phase's input vector staged once in LDS.  A row's total is a
+// wavefront sum (VALU only: v_permlane32/16_swap, DPP) and lane 0 does its epilogue, so the
+// ~300 chunks of a token need no workgroup barrier; only SwiGLU (pairs of rows on two
+// wavefronts) and the lm_head argmax combine wavefronts, once at the end of their phase.
+// Rows wider than 512 float4 (the down projection) are split into segments of 512 that the
+// owning wavefront accumulates.
 //
 // Cross-workgroup data (qkv, x, act, the KV cache rows, the argmax candidates) is written and
 // read with agent-scope relaxed atomics, i.e. stores and loads that go to the device-coherent
@@ -158,185 +162,109 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
     return s;
 }
 
-// Chunk of CH rows [rc, rc + CH) of a row-major [rows][K4] float4 matrix: thread t holds
-// columns t + NT*j (j < J) of each row.  Every slot is loaded unconditionally (a branch would
-// make the register allocator copy the previous chunk's values, which waits for their loads):
-// rows >= r1 read the zero row instead (a few KB that stay in L2), columns >= K4 are clamped
-// to the last column (the vector slice is zero there).  Row bases are uniform, per-thread
-// offsets 32-bit.
-template <int J, int CH>
+// Chunk: 8 rows, row rc + w for wavefront w, of a row-major [rows][K4] float4 matrix, segment
+// `seg` of the columns: lane l holds columns seg * 512 + l + 64 i (i < NB), so one load
+// instruction of a wavefront reads 1 KB of one row.  Every slot is loaded unconditionally:
+// rows >= r1 read the zero row (a few KB that stay in L2), columns >= K4 are clamped to the
+// last column (the staged vector is zero there).  The row base is uniform per wavefront.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ void load_chunk(float4 (&b)[NB], const float* __restrict__ W, int K4,
-                                           int rc, int r1, const float* zero_row) {
-    static_assert(J * CH <= NB, "chunk exceeds the slot budget");
-    const unsigned t = threadIdx.x;
+                                           int rc, int seg, int r1, const float* zero_row) {
+    // The lane's byte offset passes through an empty asm, so the per-slot offsets derived from
+    // it are formed at each load (two VALU operations) instead of being hoisted out of the
+    // token loop as 64-bit values, which the compiler then spills.
+    unsigned l16 = (threadIdx.x & 63) * 16u;
+    asm volatile("" : "+v"(l16));
+    const int row = rc + wave_id();
+    const float* rowp = row < r1 ? W + (size_t)row * (size_t)K4 * 4 : zero_row;
+    const unsigned lim = ((unsigned)K4 - 1u) * 16u;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-        const float* row = rc + i < r1 ? W + (size_t)(rc + i) * (size_t)K4 * 4 : zero_row;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const unsigned c = min(t + (unsigned)(NT * j), (unsigned)K4 - 1u);
-            b[i * J + j] = ldw_at(row, c * 16u);
-        }
-    }
+    for (int i = 0; i < NB; ++i)
+        b[i] = ldw_at(rowp, min(l16 + (unsigned)(seg * NB * 64 + 64 * i) * 16u, lim));
 }
 
-// Eight per-thread partial sums -> eight wavefront totals, all in VALU cross-lane operations:
-// each step halves the values a lane carries while doubling the lanes summed (lane bit 5 by
-// v_permlane32_swap, bit 4 by v_permlane16_swap, bit 3 by a DPP row rotation), then a DPP
-// shift tree sums lanes 8r .. 8r+7 into lane 8r.  Lane 8r ends with the total of row r, added
-// in the same order as an xor butterfly.
-__device__ __forceinline__ float reduce8(const float (&v)[8], int lane) {
-    float a[4];
+// This lane's part of the chunk row's dot product with the staged vector segment xn (LDS).
+__device__ __forceinline__ float chunk_dot(const float4 (&b)[NB], const float4* xn) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // lanes < 32: v[i] of lanes l and l + 32; lanes >= 32: v[i + 4] of lanes l - 32 and l
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]),
-                                                        __float_as_uint(v[i + 4]), false, false);
-        a[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    float c[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        // even rows of 16 lanes: a[i] of lanes l and l + 16; odd rows: a[i + 2]
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[i]),
-                                                        __float_as_uint(a[i + 2]), false, false);
-        c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    const bool b3 = lane & 8;
-    const float keep = b3 ? c[1] : c[0];
-    const float send = b3 ? c[0] : c[1];
-    float w = keep + dpp<0x128>(send);  // row_ror:8 = lane ^ 8 within a row
-    w += dpp<0x104>(w);                 // row_shl:4: lane l += lane l + 4
-    w += dpp<0x102>(w);                 // row_shl:2
-    w += dpp<0x101>(w);                 // row_shl:1
-    return w;
+    for (int i = 0; i < NB; ++i) s += dot4(b[i], xn[lane + 64 * i]);
+    return s;
 }
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 struct Epi {
-    unsigned long long* prof;  // profile only (null otherwise)
-    int prof_it, prof_kb, prof_nb;
     float* out;
     const float* resid;  // EPI_RESID: LDS copy of the vector added per row
-    float best;          // EPI_LOGITS: running max / index (thread 0)
+    float* rows;         // EPI_SWIGLU: LDS row results, indexed from row0
+    int row0;
+    float best;          // EPI_LOGITS: this wavefront's running max / index
     int best_idx;
 };
 
-__device__ __forceinline__ void stamp_in(const Epi& e, int which) {
-    if (e.prof && threadIdx.x == 0 && which < 16)
-        e.prof[((size_t)(e.prof_it * e.prof_nb + e.prof_kb) * 16 + which) * gridDim.x +
-               blockIdx.x] = wall_clock64();
-}
-
-// A chunk is consumed in two steps so that the registers of `b` can be refilled in between:
-// chunk_dots forms this thread's partial dot products of the CH rows, chunk_reduce does the
-// workgroup reduction and the epilogue for rows rc..rc+CH-1 (`red` is [2][NW][8] floats,
-// alternated by `rsel`).
-template <int J, int CH>
-__device__ __forceinline__ void chunk_dots(const float4 (&b)[NB], const float4 (&xv)[J],
-                                           float (&v)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CH; ++i)
-#pragma unroll
-        for (int j = 0; j < J; ++j) v[i] += dot4(b[i * J + j], xv[j]);
-}
-
-template <int CH, int EPI>
-__device__ __forceinline__ void chunk_reduce(const float (&v)[8], int rc, int r1, float* red,
-                                             int& rsel, Epi& e) {
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    float w = reduce8(v, lane);
-    float* rb = red + rsel * (NW * 8);
-    rsel ^= 1;
-    if ((lane & 7) == 0) rb[wave * 8 + (lane >> 3)] = w;
-    __syncthreads();
-    if constexpr (EPI == EPI_SWIGLU) {
-        if (t < CH / 2) {
-            float g = 0.0f, u = 0.0f;
-#pragma unroll
-            for (int q = 0; q < NW; ++q) {
-                g += rb[q * 8 + 2 * t];
-                u += rb[q * 8 + 2 * t + 1];
-            }
-            const int r = rc + 2 * t;
-            if (r + 1 < r1) st_coh(e.out + (r >> 1), (g * (1.0f / (1.0f + expf(-g)))) * u);
-        }
-    } else if constexpr (EPI == EPI_LOGITS) {
-        if (t < 64) {  // wave 0: lanes < CH own one row each
-            float s = -FLT_MAX;
-            int idx = 0x7fffffff;
-            const int r = rc + t;
-            if (t < CH && r < r1) {
-                s = 0.0f;
-#pragma unroll
-                for (int q = 0; q < NW; ++q) s += rb[q * 8 + t];
-                e.out[r] = s;
-                idx = r;
-            }
-#pragma unroll
-            for (int o = 4; o > 0; o >>= 1) {  // rows of the chunk sit in lanes 0..7
-                float os = __shfl_xor(s, o);
-                int oi = __shfl_xor(idx, o);
-                if (os > s || (os == s && oi < idx)) { s = os; idx = oi; }
-            }
-            if (t == 0 && (s > e.best || (s == e.best && idx < e.best_idx))) {
-                e.best = s;
-                e.best_idx = idx;
-            }
-        }
+// A row is complete: its total (in every lane), then the epilogue (lane 0 stores).
+template <int EPI>
+__device__ __forceinline__ void row_done(float part, int row, int r1, Epi& e) {
+    const float s = wave_sum(part);
+    if (row >= r1) return;  // uniform over the wavefront
+    const bool l0 = (threadIdx.x & 63) == 0;
+    if constexpr (EPI == EPI_STORE) {
+        if (l0) st_coh(e.out + row, s);
+    } else if constexpr (EPI == EPI_RESID) {
+        if (l0) st_coh(e.out + row, s + e.resid[row]);
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        if (l0) e.rows[row - e.row0] = s;
     } else {
-        if (t < CH) {
-            const int r = rc + t;
-            if (r < r1) {
-                float s = 0.0f;
-#pragma unroll
-                for (int q = 0; q < NW; ++q) s += rb[q * 8 + t];
-                if constexpr (EPI == EPI_RESID) s += e.resid[r];
-                st_coh(e.out + r, s);
-            }
+        if (l0) e.out[row] = s;
+        if (s > e.best || (s == e.best && row < e.best_idx)) {
+            e.best = s;
+            e.best_idx = row;
         }
     }
 }
 
-template <int J, int CH, int EPI>
-__device__ __forceinline__ void chunk_step(const float4 (&b)[NB], const float4 (&xv)[J], int rc,
-                                           int r1, float* red, int& rsel, Epi& e) {
-    float v[8];
-    chunk_dots<J, CH>(b, xv, v);
-    chunk_reduce<CH, EPI>(v, rc, r1, red, rsel, e);
-}
-
-// Rows [r0, r1) of W (row-major, K4 float4 per row) against the per-thread vector slice xv.
-// On entry b0 holds chunk 0 and, when PRE == 2, b1 holds chunk 1 (issued by the caller,
-// usually before a barrier); chunk c+3 is issued into a register set as soon as the dot
-// products of chunk c have read it, before chunk c's reduction, in three rotating sets.
-template <int J, int CH, int EPI, int PRE = 2>
-__device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4, int r0, int r1,
-                                            const float4 (&xv)[J], float4 (&b0)[NB],
-                                            float4 (&b1)[NB], float4 (&b2)[NB], float* red,
-                                            int& rsel, Epi& e, const float* zero_row) {
-    const int nch = (r1 - r0 + CH - 1) / CH;
-    if constexpr (PRE == 1) load_chunk<J, CH>(b1, W, K4, r0 + CH, r1, zero_row);
-    load_chunk<J, CH>(b2, W, K4, r0 + 2 * CH, r1, zero_row);
-    float v[8];
-    for (int c = 0; c < nch; c += 3) {
-        chunk_dots<J, CH>(b0, xv, v);
-        load_chunk<J, CH>(b0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + c * CH, r1, red, rsel, e);
-        if (c + 1 >= nch) break;
-        chunk_dots<J, CH>(b1, xv, v);
-        load_chunk<J, CH>(b1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
-        if (c + 2 >= nch) break;
-        chunk_dots<J, CH>(b2, xv, v);
-        load_chunk<J, CH>(b2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
+// One chunk of a stream: its dot products, the refill of its registers with chunk q + 3 (so
+// the load pipe stays full while this chunk's row is reduced), and, on the row's last
+// segment, the row's epilogue.
+template <int EPI, int NSEG>
+__device__ __forceinline__ void stream_step(float4 (&b)[NB], int q, const float* __restrict__ W,
+                                            int K4, int r0, int r1, const float4* xn, float& acc,
+                                            Epi& e, const float* zero_row) {
+    const int rg = q / NSEG, seg = q - rg * NSEG;
+    // The vector reads stay in the loop: hoisted (they are loop-invariant per register set),
+    // they would hold 32 VGPRs per segment for the whole stream.
+    asm volatile("" ::: "memory");
+    acc += chunk_dot(b, xn + seg * NB * 64);
+    const int q3 = q + 3, rg3 = q3 / NSEG;
+    load_chunk(b, W, K4, r0 + 8 * rg3, q3 - rg3 * NSEG, r1, zero_row);
+    if (seg == NSEG - 1) {
+        row_done<EPI>(acc, r0 + 8 * rg + wave_id(), r1, e);
+        acc = 0.0f;
     }
 }
 
+// Rows [r0, r1) of W against the staged vector xn (NSEG segments of 512 float4), in chunks
+// q = 0 .. nq-1 (row group q / NSEG, segment q % NSEG) rotating over three register sets.
+// On entry b0 holds chunk 0, b1 chunk 1 when PRE >= 2, b2 chunk 2 when PRE == 3.
+template <int EPI, int NSEG, int PRE>
+__device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4, int r0, int r1,
+                                            const float4* xn, float4 (&b0)[NB],
+                                            float4 (&b1)[NB], float4 (&b2)[NB], Epi& e,
+                                            const float* zero_row) {
+    const int nq = (r1 - r0 + 7) / 8 * NSEG;
+    if constexpr (PRE == 1) load_chunk(b1, W, K4, r0 + 8 * (1 / NSEG), 1 % NSEG, r1, zero_row);
+    if constexpr (PRE <= 2) load_chunk(b2, W, K4, r0 + 8 * (2 / NSEG), 2 % NSEG, r1, zero_row);
+    float acc = 0.0f;
+    for (int q = 0; q < nq; q += 3) {
+        stream_step<EPI, NSEG>(b0, q, W, K4, r0, r1, xn, acc, e, zero_row);
+        if (q + 1 >= nq) break;
+        stream_step<EPI, NSEG>(b1, q + 1, W, K4, r0, r1, xn, acc, e, zero_row);
+        if (q + 2 >= nq) break;
+        stream_step<EPI, NSEG>(b2, q + 2, W, K4, r0, r1, xn, acc, e, zero_row);
+    }
+}
 
 // LDS chunk stage: thread t keeps float4 i of a register chunk at slot[i * NT + t]
 // (consecutive threads, consecutive 16 bytes: conflict-free), and reads back only its own.
@@ -344,53 +272,39 @@ __device__ __forceinline__ void stage_chunk(float4* slot, const float4 (&b)[NB])
 #pragma unroll
     for (int i = 0; i < NB; ++i) slot[i * NT + threadIdx.x] = b[i];
 }
-template <int CH>
-__device__ __forceinline__ void chunk_dots_lds(const float4* slot, const float4 (&xv)[1],
-                                               float (&v)[8]) {
+__device__ __forceinline__ float chunk_dot_lds(const float4* slot, const float4* xn) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) v[i] += dot4(slot[i * NT + threadIdx.x], xv[0]);
+    for (int i = 0; i < NB; ++i) s += dot4(slot[i * NT + threadIdx.x], xn[lane + 64 * i]);
+    return s;
 }
 
-// Rows [r0, r1) in chunks of CH rows, with chunks 0 .. nls-1 staged in LDS (slot c at
-// stage + c * NB * NT) and chunks nls .. nls+2 already issued into c0, c1 and c2; chunk c+3 is
-// issued into a register set as soon as the dot products of chunk c have read it.
-template <int CH, int EPI>
+// Rows [r0, r1) (one segment) with chunks 0 .. nls-1 staged in LDS (slot k at
+// stage + k * NB * NT) and chunks nls .. nls+2 already issued into c0, c1 and c2: the resident
+// register chunks first, so that chunk nls + 3 streams from the start, then the LDS chunks.
+template <int EPI>
 __device__ __forceinline__ void stream_rows_staged(const float* __restrict__ W, int K4, int r0,
                                                    int r1, int nls, const float4* stage,
-                                                   const float4 (&xv)[1], float4 (&c0)[NB],
-                                                   float4 (&c1)[NB], float4 (&c2)[NB],
-                                                   float* red, int& rsel, Epi& e,
+                                                   const float4* xn, float4 (&c0)[NB],
+                                                   float4 (&c1)[NB], float4 (&c2)[NB], Epi& e,
                                                    const float* zero_row) {
-    const int nch = (r1 - r0 + CH - 1) / CH;
-    float v[8];
-    // The resident register chunks first, so that chunk nls + 3 streams from the start.
+    const int nch = (r1 - r0 + 7) / 8;
+    const int w = wave_id();
     for (int c = nls; c < nch; c += 3) {
-        chunk_dots<1, CH>(c0, xv, v);
-        load_chunk<1, CH>(c0, W, K4, r0 + (c + 3) * CH, r1, zero_row);
-        chunk_reduce<CH, EPI>(v, r0 + c * CH, r1, red, rsel, e);
+        float acc = 0.0f;
+        stream_step<EPI, 1>(c0, c, W, K4, r0, r1, xn, acc, e, zero_row);
         if (c + 1 < nch) {
-            chunk_dots<1, CH>(c1, xv, v);
-            load_chunk<1, CH>(c1, W, K4, r0 + (c + 4) * CH, r1, zero_row);
-            chunk_reduce<CH, EPI>(v, r0 + (c + 1) * CH, r1, red, rsel, e);
-            if (c + 2 < nch) {
-                chunk_dots<1, CH>(c2, xv, v);
-                load_chunk<1, CH>(c2, W, K4, r0 + (c + 5) * CH, r1, zero_row);
-                chunk_reduce<CH, EPI>(v, r0 + (c + 2) * CH, r1, red, rsel, e);
-            }
+            stream_step<EPI, 1>(c1, c + 1, W, K4, r0, r1, xn, acc, e, zero_row);
+            if (c + 2 < nch) stream_step<EPI, 1>(c2, c + 2, W, K4, r0, r1, xn, acc, e, zero_row);
         }
         if (c == nls) {
-            for (int k = 0; k < nls; ++k) {
-                chunk_dots_lds<CH>(stage + k * NB * NT, xv, v);
-                chunk_reduce<CH, EPI>(v, r0 + k * CH, r1, red, rsel, e);
-            }
+            for (int k = 0; k < nls; ++k)
+                row_done<EPI>(chunk_dot_lds(stage + k * NB * NT, xn), r0 + 8 * k + w, r1, e);
         }
     }
-    for (int k = 0; k < nls && k < nch && nch <= nls; ++k) {
-        chunk_dots_lds<CH>(stage + k * NB * NT, xv, v);
-        chunk_reduce<CH, EPI>(v, r0 + k * CH, r1, red, rsel, e);
-    }
+    for (int k = 0; k < nls && k < nch && nch <= nls; ++k)
+        row_done<EPI>(chunk_dot_lds(stage + k * NB * NT, xn), r0 + 8 * k + w, r1, e);
 }
 
 // Grid barrier, split so the caller can issue loads between arrival and wait.
@@ -448,7 +362,8 @@ __device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long lon
 // RMSNorm of the vector slice, in two steps so weight loads can be issued between them:
 // norm_load issues this thread's float4 of x (device-coherent unless it is a read-only row,
 // the embedding) and keeps it in xs (LDS) for the residual add of the next phase;
-// norm_finish forms xv = (x * rsqrt(mean(x^2) + eps)) * w.  K4 <= NT.
+// norm_finish writes xn = (x * rsqrt(mean(x^2) + eps)) * w to LDS (zero beyond K) and
+// synchronises the workgroup.  K4 <= NT.
 struct NormIn {
     float4 x, w;
 };
@@ -465,7 +380,7 @@ __device__ __forceinline__ NormIn norm_load(const float* __restrict__ x, bool co
     return r;
 }
 __device__ __forceinline__ void norm_finish(NormIn in, int K, float eps, float* scratch,
-                                            float* xs, float4 (&xv)[1]) {
+                                            float* xs, float4* xn) {
     const int t = threadIdx.x;
     float4 v = in.x;
     if (t < K / 4) *reinterpret_cast<float4*>(xs + 4 * t) = v;
@@ -476,7 +391,8 @@ __device__ __forceinline__ void norm_finish(NormIn in, int K, float eps, float* 
         v = make_float4((v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z,
                         (v.w * inv) * g.w);
     }
-    xv[0] = v;
+    xn[t] = v;  // zero beyond K
+    __syncthreads();
 }
 
 // Phase timestamp for the optional profile buffer (thread 0 of each workgroup).
@@ -488,6 +404,8 @@ __device__ __forceinline__ void stamp(const PersistArgs& a, int it, int k, int w
 }
 
 constexpr int KSTRIDE = 68;  // LDS row stride of staged K rows: conflict-free 16-byte reads
+constexpr int GU_ROWS = 448;   // gate/up rows of one workgroup kept in LDS (persist_plan checks)
+constexpr int LDS_MISC = 512;  // floats before the hidden-sized residual copy
 
 __device__ __forceinline__ float lane_bcast(float v, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
@@ -621,15 +539,18 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
 template <int JF>
 __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    constexpr int CHF = NB / JF;  // rows per chunk of the down projection
     const int qd = a.n_heads * 64;
-    float* red = lds;                        // [2][NW][8]
-    float* scratch = lds + 2 * NW * 8;       // [NW] block sums
-    int* okw = reinterpret_cast<int*>(lds + 160);  // [NW] barrier wait results
-    float* best_v = scratch + NW + 4;        // global argmax staging
-    int* best_i = reinterpret_cast<int*>(best_v + NW);
-    float* xs = lds + 256;                   // [hidden] raw x of the last norm (residual)
-    float* kv_s = xs + a.hidden;             // attention staging (attention_heads)
+    float* scratch = lds;                                  // [NW] block sums
+    int* okw = reinterpret_cast<int*>(lds + 16);           // [NW] barrier wait results
+    float* best_v = lds + 32;                              // [NW] argmax staging
+    int* best_i = reinterpret_cast<int*>(lds + 48);        // [NW]
+    float* gu_rows = lds + 64;                             // [GU_ROWS] gate/up row results
+    float* xs = lds + LDS_MISC;                            // [hidden] raw x of the last norm
+    float4* xn = reinterpret_cast<float4*>(xs + a.hidden);  // [512] the phase's input vector
+    float* region = reinterpret_cast<float*>(xn + NB * 64);
+    float* kv_s = region;                                  // attention staging (B1)
+    float4* stage = reinterpret_cast<float4*>(region);      // gate/up LDS chunks (B1 .. C)
+    float4* act_s = reinterpret_cast<float4*>(region);      // the down phase's input (D)
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int b = blockIdx.x, G = gridDim.x;
@@ -649,7 +570,6 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
         b1[i] = b0[i];
         b2[i] = b0[i];
     }
-    int rsel = 0;
     unsigned long long target = a.bar_base;
     // uniform over the workgroup; readfirstlane lets the compiler keep them (and everything
     // derived from them) in scalar registers
@@ -657,14 +577,12 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
     int step = __builtin_amdgcn_readfirstlane(a.st->step);
     int token = __builtin_amdgcn_readfirstlane(a.forced_token >= 0 ? a.forced_token : a.st->token);
 
-
     const bool attn_wg = b < a.n_heads;  // this workgroup computes an attention head
     // The other workgroups stage gate/up chunks 0 and 1 in LDS (over the attention staging,
     // which they do not use) during the attention phase.
     const int nls = attn_wg ? 0 : 2;
-    float4* stage = reinterpret_cast<float4*>(kv_s);
-    load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
-    load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
+    load_chunk(b0, a.layers[0].wqkv, H4, qa0, 0, qa1, a.zero_row);
+    load_chunk(b1, a.layers[0].wqkv, H4, qa0 + 8, 0, qa1, a.zero_row);
     for (int it = 0; it < a.n_tokens; ++it) {
         const float* erow = a.embed + (int64_t)token * H;
         int kb = 0;  // barrier index within the token (profile only)
@@ -682,18 +600,18 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             // ---- A: qkv (at most two chunks, both resident) -------------------------------
             {
                 NormIn xr = norm_load(xin, l != 0, H, L.attn_norm);
-                load_chunk<1, 8>(b2, L.wo, Q4, h0, h1, a.zero_row);
-                float4 xv[1];
-                norm_finish(xr, H, a.eps, scratch, xs, xv);
+                load_chunk(b2, L.wo, Q4, h0, 0, h1, a.zero_row);
+                norm_finish(xr, H, a.eps, scratch, xs, xn);
                 e.out = a.qkv;
-                chunk_step<1, 8, EPI_STORE>(b0, xv, qa0, qa1, red, rsel, e);
-                chunk_step<1, 8, EPI_STORE>(b1, xv, qa0 + 8, qa1, red, rsel, e);
+                const int w = wave_id();
+                row_done<EPI_STORE>(chunk_dot(b0, xn), qa0 + w, qa1, e);
+                row_done<EPI_STORE>(chunk_dot(b1, xn), qa0 + 8 + w, qa1, e);
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
             if (!attn_wg) {
-                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
-                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+                load_chunk(b0, L.w_gu, H4, 2 * p0, 0, 2 * p1, a.zero_row);
+                load_chunk(b1, L.w_gu, H4, 2 * p0 + 8, 0, 2 * p1, a.zero_row);
             }
             target += 1;
             if (!bar_wait(a, target, okw)) return;
@@ -703,59 +621,73 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
             if (attn_wg) {
-                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0, 2 * p1, a.zero_row);
-                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 8, 2 * p1, a.zero_row);
+                load_chunk(b0, L.w_gu, H4, 2 * p0, 0, 2 * p1, a.zero_row);
+                load_chunk(b1, L.w_gu, H4, 2 * p0 + 8, 0, 2 * p1, a.zero_row);
             } else {
                 stage_chunk(stage, b0);
-                load_chunk<1, 8>(b0, L.w_gu, H4, 2 * p0 + 16, 2 * p1, a.zero_row);
+                load_chunk(b0, L.w_gu, H4, 2 * p0 + 16, 0, 2 * p1, a.zero_row);
                 stage_chunk(stage + NB * NT, b1);
-                load_chunk<1, 8>(b1, L.w_gu, H4, 2 * p0 + 24, 2 * p1, a.zero_row);
+                load_chunk(b1, L.w_gu, H4, 2 * p0 + 24, 0, 2 * p1, a.zero_row);
             }
             target += 1;
             if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- B2: Wo + residual (one chunk: h1 - h0 <= 8) ------------------------------
             {
-                float4 xv[1];
-                xv[0] = t < Q4 ? ld_coh4_at(a.att, (unsigned)t * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                xn[t] = t < Q4 ? ld_coh4_at(a.att, (unsigned)t * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                __syncthreads();
                 e.out = a.x;
                 e.resid = xs;
-                chunk_step<1, 8, EPI_RESID>(b2, xv, h0, h1, red, rsel, e);
+                row_done<EPI_RESID>(chunk_dot(b2, xn), h0 + wave_id(), h1, e);
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
-            load_chunk<1, 8>(b2, L.w_gu, H4, 2 * p0 + 8 * (nls + 2), 2 * p1, a.zero_row);
+            load_chunk(b2, L.w_gu, H4, 2 * p0 + 8 * (nls + 2), 0, 2 * p1, a.zero_row);
             target += 1;
             if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- C: gate/up + SwiGLU ------------------------------------------------------
             {
                 NormIn xr = norm_load(a.x, true, H, L.ffn_norm);
-                float4 xv[1];
-                norm_finish(xr, H, a.eps, scratch, xs, xv);
-                e.out = a.act;
-                stream_rows_staged<8, EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, nls, stage, xv, b0,
-                                                  b1, b2, red, rsel, e, a.zero_row);
+                norm_finish(xr, H, a.eps, scratch, xs, xn);
+                e.rows = gu_rows;
+                e.row0 = 2 * p0;
+                stream_rows_staged<EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, nls, stage, xn, b0, b1,
+                                               b2, e, a.zero_row);
+                __syncthreads();  // every row result of the workgroup is in gu_rows
+                for (int i = t; i < p1 - p0; i += NT) {
+                    const float g = gu_rows[2 * i], u = gu_rows[2 * i + 1];
+                    st_coh(a.act + p0 + i, (g * (1.0f / (1.0f + expf(-g)))) * u);
+                }
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
-            load_chunk<JF, CHF>(b0, L.w_down, F4, h0, h1, a.zero_row);
-            load_chunk<JF, CHF>(b1, L.w_down, F4, h0 + CHF, h1, a.zero_row);
+            load_chunk(b0, L.w_down, F4, h0, 0, h1, a.zero_row);
+            load_chunk(b1, L.w_down, F4, h0 + 8 * (1 / JF), 1 % JF, h1, a.zero_row);
             target += 1;
             if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- D: down + residual -------------------------------------------------------
             {
-                float4 xv[JF];
 #pragma unroll
                 for (int jj = 0; jj < JF; ++jj) {
                     const int c = t + NT * jj;
-                    xv[jj] = c < F4 ? ld_coh4_at(a.act, (unsigned)c * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    act_s[c] = c < F4 ? ld_coh4_at(a.act, (unsigned)c * 16u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 }
+                __syncthreads();
                 e.out = a.x;
                 e.resid = xs;
-                stream_rows<JF, CHF, EPI_RESID>(L.w_down, F4, h0, h1, xv, b0, b1, b2, red, rsel,
-                                                e, a.zero_row);
+                // one row group (h1 - h0 <= 8): JF segment chunks, summed in segment order
+                if constexpr (JF <= 3) {
+                    if constexpr (JF == 3) load_chunk(b2, L.w_down, F4, h0, 2, h1, a.zero_row);
+                    float acc = chunk_dot(b0, act_s);
+                    if constexpr (JF >= 2) acc += chunk_dot(b1, act_s + NB * 64);
+                    if constexpr (JF == 3) acc += chunk_dot(b2, act_s + 2 * NB * 64);
+                    row_done<EPI_RESID>(acc, h0 + wave_id(), h1, e);
+                } else {
+                    stream_rows<EPI_RESID, JF, 2>(L.w_down, F4, h0, h1, act_s, b0, b1, b2, e,
+                                                  a.zero_row);
+                }
             }
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
@@ -764,8 +696,8 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                 const bool last = l + 1 == a.n_layers;
                 const float* Wn = last ? a.lm_head : a.layers[last ? l : l + 1].wqkv;
                 const int n0 = last ? v0 : qa0, n1 = last ? v1 : qa1;
-                load_chunk<1, 8>(b0, Wn, H4, n0, n1, a.zero_row);
-                load_chunk<1, 8>(b1, Wn, H4, n0 + 8, n1, a.zero_row);
+                load_chunk(b0, Wn, H4, n0, 0, n1, a.zero_row);
+                load_chunk(b1, Wn, H4, n0 + 8, 0, n1, a.zero_row);
             }
             target += 1;
             if (!bar_wait(a, target, okw)) return;
@@ -774,27 +706,35 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
         // ---- E: lm_head + per-workgroup argmax ---------------------------------------------
         {
             NormIn xr = norm_load(a.x, true, H, a.final_norm);
-            float4 xv[1];
-            norm_finish(xr, H, a.eps, scratch, xs, xv);
+            norm_finish(xr, H, a.eps, scratch, xs, xn);
             Epi e{};
             e.out = a.logits;
             e.best = -FLT_MAX;
             e.best_idx = 0x7fffffff;
-            stream_rows<1, 8, EPI_LOGITS>(a.lm_head, H4, v0, v1, xv, b0, b1, b2, red, rsel, e,
-                                          a.zero_row);
+            stream_rows<EPI_LOGITS, 1, 2>(a.lm_head, H4, v0, v1, xn, b0, b1, b2, e, a.zero_row);
+            const int w = wave_id();
+            if ((t & 63) == 0) {
+                best_v[w] = e.best;
+                best_i[w] = e.best_idx;
+            }
+            __syncthreads();
             if (t == 0) {
+                float s = best_v[0];
+                int idx = best_i[0];
+                for (int q = 1; q < NW; ++q)
+                    if (best_v[q] > s || (best_v[q] == s && best_i[q] < idx)) { s = best_v[q]; idx = best_i[q]; }
                 const unsigned long long packed =
-                    (unsigned long long)__float_as_uint(e.best) |
-                    ((unsigned long long)(unsigned)e.best_idx << 32);
+                    (unsigned long long)__float_as_uint(s) | ((unsigned long long)(unsigned)idx << 32);
                 __hip_atomic_store(reinterpret_cast<unsigned long long*>(a.cand + b), packed,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            __syncthreads();  // best_v / best_i are reused by the global argmax
         }
         stamp(a, it, kb, 0);
         bar_arrive(a.flags, target + 1);
         // qkv chunks of layer 0 for the next token (after the last token they go unused)
-        load_chunk<1, 8>(b0, a.layers[0].wqkv, H4, qa0, qa1, a.zero_row);
-        load_chunk<1, 8>(b1, a.layers[0].wqkv, H4, qa0 + 8, qa1, a.zero_row);
+        load_chunk(b0, a.layers[0].wqkv, H4, qa0, 0, qa1, a.zero_row);
+        load_chunk(b1, a.layers[0].wqkv, H4, qa0 + 8, 0, qa1, a.zero_row);
         target += 1;
         if (!bar_wait(a, target, okw)) return;
         stamp(a, it, kb++, 1);
@@ -857,9 +797,13 @@ const void* pick_kernel(int jf) {
 
 
 size_t lds_bytes(const PersistArgs& a) {
+    const int jf = (a.ffn / 4 + NT - 1) / NT;
     const size_t att = 64 * KSTRIDE + 64 * 64 + 4 * 64 + NW * 64;
-    const size_t staged = 2 * NB * NT * 4;  // two gate/up chunks (float4 per thread per row)
-    size_t floats = 256 + (size_t)a.hidden + (att > staged ? att : staged);
+    const size_t staged = 2 * NB * NT * 4;  // two gate/up chunks
+    const size_t act = (size_t)jf * NB * 64 * 4;
+    size_t region = att > staged ? att : staged;
+    if (act > region) region = act;
+    const size_t floats = LDS_MISC + (size_t)a.hidden + NB * 64 * 4 + region;
     return floats * sizeof(float);
 }
 
@@ -902,6 +846,16 @@ int persist_plan(int device, PersistArgs* ap, int* grid, size_t* lds, std::strin
         return no("more than 8 hidden rows per workgroup (hidden > 8 x CUs)");
     if (((a.n_heads + 2 * a.n_kv) * 64 + cus - 1) / cus > 16)
         return no("more than 16 qkv rows per workgroup");
+    {
+        // gate/up rows per workgroup (the kernel's 1:2 split) must fit the LDS row buffer
+        const int64_t na = std::min(a.n_heads, cus);
+        auto cw = [&](int64_t i) { return i <= na ? i : na + 2 * (i - na); };
+        const int64_t tot = cw(cus);
+        for (int b = 0; b < cus; ++b) {
+            const int64_t rows = 2 * ((int64_t)a.ffn * cw(b + 1) / tot - (int64_t)a.ffn * cw(b) / tot);
+            if (rows > GU_ROWS) return no("too many gate/up rows per workgroup");
+        }
+    }
     *grid = cus;  // one workgroup per CU
     *lds = bytes;
     return SHP_OK;
