@@ -229,16 +229,19 @@ __device__ __forceinline__ void row_done(float part, int row, int r1, Epi& e) {
 // the load pipe stays full while this chunk's row is reduced), and, on the row's last
 // segment, the row's epilogue.
 template <int EPI, int NSEG>
-__device__ __forceinline__ void stream_step(float4 (&b)[NB], int q, const float* __restrict__ W,
-                                            int K4, int r0, int r1, const float4* xn, float& acc,
-                                            Epi& e, const float* zero_row) {
+__device__ __forceinline__ void stream_step(float4 (&b)[NB], int q, int nq,
+                                            const float* __restrict__ W, int K4, int r0, int r1,
+                                            const float4* xn, float& acc, Epi& e,
+                                            const float* zero_row) {
     const int rg = q / NSEG, seg = q - rg * NSEG;
     // The vector reads stay in the loop: hoisted (they are loop-invariant per register set),
     // they would hold 32 VGPRs per segment for the whole stream.
     asm volatile("" ::: "memory");
     acc += chunk_dot(b, xn + seg * NB * 64);
     const int q3 = q + 3, rg3 = q3 / NSEG;
-    load_chunk(b, W, K4, r0 + 8 * rg3, q3 - rg3 * NSEG, r1, zero_row);
+    // past the last chunk nothing is loaded: those loads would only delay this workgroup's
+    // barrier arrival, which waits for every load issued before its stores
+    if (q3 < nq) load_chunk(b, W, K4, r0 + 8 * rg3, q3 - rg3 * NSEG, r1, zero_row);
     if (seg == NSEG - 1) {
         row_done<EPI>(acc, r0 + 8 * rg + wave_id(), r1, e);
         acc = 0.0f;
@@ -254,15 +257,17 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ W, int K4,
                                             float4 (&b1)[NB], float4 (&b2)[NB], Epi& e,
                                             const float* zero_row) {
     const int nq = (r1 - r0 + 7) / 8 * NSEG;
-    if constexpr (PRE == 1) load_chunk(b1, W, K4, r0 + 8 * (1 / NSEG), 1 % NSEG, r1, zero_row);
-    if constexpr (PRE <= 2) load_chunk(b2, W, K4, r0 + 8 * (2 / NSEG), 2 % NSEG, r1, zero_row);
+    if constexpr (PRE == 1)
+        if (nq > 1) load_chunk(b1, W, K4, r0 + 8 * (1 / NSEG), 1 % NSEG, r1, zero_row);
+    if constexpr (PRE <= 2)
+        if (nq > 2) load_chunk(b2, W, K4, r0 + 8 * (2 / NSEG), 2 % NSEG, r1, zero_row);
     float acc = 0.0f;
     for (int q = 0; q < nq; q += 3) {
-        stream_step<EPI, NSEG>(b0, q, W, K4, r0, r1, xn, acc, e, zero_row);
+        stream_step<EPI, NSEG>(b0, q, nq, W, K4, r0, r1, xn, acc, e, zero_row);
         if (q + 1 >= nq) break;
-        stream_step<EPI, NSEG>(b1, q + 1, W, K4, r0, r1, xn, acc, e, zero_row);
+        stream_step<EPI, NSEG>(b1, q + 1, nq, W, K4, r0, r1, xn, acc, e, zero_row);
         if (q + 2 >= nq) break;
-        stream_step<EPI, NSEG>(b2, q + 2, W, K4, r0, r1, xn, acc, e, zero_row);
+        stream_step<EPI, NSEG>(b2, q + 2, nq, W, K4, r0, r1, xn, acc, e, zero_row);
     }
 }
 
@@ -293,10 +298,10 @@ __device__ __forceinline__ void stream_rows_staged(const float* __restrict__ W, 
     const int w = wave_id();
     for (int c = nls; c < nch; c += 3) {
         float acc = 0.0f;
-        stream_step<EPI, 1>(c0, c, W, K4, r0, r1, xn, acc, e, zero_row);
+        stream_step<EPI, 1>(c0, c, nch, W, K4, r0, r1, xn, acc, e, zero_row);
         if (c + 1 < nch) {
-            stream_step<EPI, 1>(c1, c + 1, W, K4, r0, r1, xn, acc, e, zero_row);
-            if (c + 2 < nch) stream_step<EPI, 1>(c2, c + 2, W, K4, r0, r1, xn, acc, e, zero_row);
+            stream_step<EPI, 1>(c1, c + 1, nch, W, K4, r0, r1, xn, acc, e, zero_row);
+            if (c + 2 < nch) stream_step<EPI, 1>(c2, c + 2, nch, W, K4, r0, r1, xn, acc, e, zero_row);
         }
         if (c == nls) {
             for (int k = 0; k < nls; ++k)
