@@ -61,6 +61,9 @@ struct PersistArgs {
     float* v_cache;
     float* x;       // [hidden] residual stream
     float* qkv;     // [(n_heads + 2 n_kv) * 64]
+    // [(n_heads + 2 n_kv) * 64] the qkv rows as tagged words, (phase epoch << 32) | float bits:
+    // attention waits for its head's words instead of a grid barrier
+    unsigned long long* qkv_tag;
     float* att;     // [n_heads * 64] attention output
     float* act;     // [ffn] silu(gate) * up
     float* logits;  // [vocab]

@@ -193,7 +193,7 @@ __device__ __forceinline__ float chunk_dot(const float4 (&b)[NB], const float4* 
     return s;
 }
 
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3, EPI_QKV = 4 };
 
 struct Epi {
     float* out;
@@ -202,6 +202,8 @@ struct Epi {
     int row0;
     float best;          // EPI_LOGITS: this wavefront's running max / index
     int best_idx;
+    unsigned long long* tag;  // EPI_QKV: tagged copy of each row, (epoch << 32) | float bits
+    unsigned epoch;
 };
 
 // A row is complete: its total (in every lane), then the epilogue (lane 0 stores).
@@ -212,6 +214,13 @@ __device__ __forceinline__ void row_done(float part, int row, int r1, Epi& e) {
     const bool l0 = (threadIdx.x & 63) == 0;
     if constexpr (EPI == EPI_STORE) {
         if (l0) st_coh(e.out + row, s);
+    } else if constexpr (EPI == EPI_QKV) {
+        if (l0) {
+            st_coh(e.out + row, s);
+            __hip_atomic_store((SHP_GLOBAL unsigned long long*)(e.tag + row),
+                               ((unsigned long long)e.epoch << 32) | __float_as_uint(s),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     } else if constexpr (EPI == EPI_RESID) {
         if (l0) st_coh(e.out + row, s + e.resid[row]);
     } else if constexpr (EPI == EPI_SWIGLU) {
@@ -453,9 +462,12 @@ __device__ __forceinline__ void stage_kv_tile0(const PersistArgs& a, int l, int 
 }
 
 // pre: tile 0 of the first head (h = blockIdx.x) is already in kv_s (stage_kv_tile0, followed
-// by a workgroup barrier).
-__device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int pos,
-                                                float* kv_s, int it, int kb, bool pre) {
+// by a workgroup barrier).  q, k and v of the current position are read from a.qkv_tag once
+// all 192 words carry `epoch` (the qkv phase's); false (uniformly over the workgroup) when that
+// wait gave up or another workgroup did.  okw: NW ints of LDS.
+__device__ __forceinline__ bool attention_heads(const PersistArgs& a, int l, int pos,
+                                                float* kv_s, int it, int kb, bool pre,
+                                                unsigned epoch, int* okw) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int nq = a.n_heads, nkv = a.n_kv, grp = nq / nkv, S = a.max_seq;
     const int64_t per_layer = (int64_t)nkv * S * 64;
@@ -490,11 +502,33 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
                     v4[u] = ld_coh4_at(vg, off);
                 }
             }
-            if (t0 == 0 && t < 48) {  // q_h, k_g, v_g: 3 x 16 float4
-                const int which = t >> 4, c4 = t & 15;
-                const int src = which == 0 ? h * 64 : which == 1 ? (nq + g) * 64 : (nq + nkv + g) * 64;
-                *reinterpret_cast<float4*>(cur + which * 64 + c4 * 4) =
-                    ld_coh4_at(a.qkv, (unsigned)(src + c4 * 4) * 4u);
+            if (t0 == 0) {  // q_h, k_g, v_g: wavefronts 0-2 wait for their 64 tagged words
+                int ok = 1;
+                if (t < 192) {
+                    const int which = t >> 6, d = t & 63;
+                    const int src = (which == 0 ? h : which == 1 ? nq + g : nq + nkv + g) * 64 + d;
+                    unsigned long long w = 0;
+                    long long n = 0;
+                    while (true) {
+                        w = __hip_atomic_load((SHP_GLOBAL unsigned long long*)(a.qkv_tag + src),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (__all((unsigned)(w >> 32) == epoch)) break;
+                        __builtin_amdgcn_s_sleep(1);
+                        if ((++n & 127) == 0) {
+                            if (__hip_atomic_load((SHP_GLOBAL int*)a.abort_flag, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                                n > a.spin_limit) {
+                                if (lane == 0)
+                                    __hip_atomic_store((SHP_GLOBAL int*)a.abort_flag, 1,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                ok = 0;
+                                break;
+                            }
+                        }
+                    }
+                    cur[which * 64 + d] = __uint_as_float((unsigned)w);
+                }
+                if (lane == 0) okw[wave] = ok;
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -505,7 +539,12 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
                 }
             }
             __syncthreads();
-            if (t0 == 0) stamp(a, it, kb, 2);
+            if (t0 == 0) {
+                int all = 1;
+                for (int w = 0; w < NW; ++w) all &= okw[w];
+                if (!all) return false;
+                stamp(a, it, kb, 2);
+            }
             float scale = 1.0f;
             if (wave == 0) {
                 if (t0 == 0) {
@@ -567,6 +606,7 @@ __device__ __forceinline__ void attention_heads(const PersistArgs& a, int l, int
             st_coh(a.att + h * 64 + lane, (o * scale + e * vcur) / (lsum * scale + e));
         }
     }
+    return true;
 }
 
 template <int JF>
@@ -636,14 +676,17 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                 load_chunk(b2, L.wo, Q4, h0, 0, h1, a.zero_row);
                 norm_finish(xr, H, a.eps, scratch, xs, xn);
                 e.out = a.qkv;
+                e.tag = a.qkv_tag;
+                e.epoch = (unsigned)(target + 1);
                 const int w = wave_id();
-                row_done<EPI_STORE>(chunk_dot(b0, xn), qa0 + w, qa1, e);
-                row_done<EPI_STORE>(chunk_dot(b1, xn), qa0 + 8 + w, qa1, e);
+                row_done<EPI_QKV>(chunk_dot(b0, xn), qa0 + w, qa1, e);
+                row_done<EPI_QKV>(chunk_dot(b1, xn), qa0 + 8 + w, qa1, e);
             }
+            // No grid barrier after the qkv phase: only attention consumes qkv, and it waits for
+            // the tagged words of its head (the phase's epoch is used for the tags alone).
             stamp(a, it, kb, 0);
-            bar_arrive(a.flags, target + 1);
-            // The workgroups with one attention head stage its cached K / V tile meanwhile
-            // (the poll would wait for those loads anyway).
+            // The workgroups with one attention head stage its cached K / V tile first (the
+            // tag poll would wait for those loads anyway).
             const bool pre_kv = attn_wg && G >= a.n_heads;
             if (!attn_wg) {
                 load_chunk(b0, L.w_gu, H4, 2 * p0, 0, 2 * p1, a.zero_row);
@@ -652,10 +695,10 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                 stage_kv_tile0(a, l, pos, b, kv_s);
             }
             target += 1;
-            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- B1: attention, one workgroup per query head ------------------------------
-            attention_heads(a, l, pos, kv_s, it, kb, pre_kv);
+            if (attn_wg && !attention_heads(a, l, pos, kv_s, it, kb, pre_kv, (unsigned)target, okw))
+                return;
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
             if (attn_wg) {

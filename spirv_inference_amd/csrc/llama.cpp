@@ -126,6 +126,10 @@ struct Llama {
                                          persist_flag_slots(p_grid) * sizeof(unsigned long long),
                                          ctx->stream));
             SHP_HIP_CHECK(hipMemsetAsync(abort_flag, 0, sizeof(int), ctx->stream));
+            // epochs restart at 0: tags written before the abort must not match them
+            SHP_HIP_CHECK(hipMemsetAsync(pa.qkv_tag, 0,
+                                         (size_t)qkv_rows() * sizeof(unsigned long long),
+                                         ctx->stream));
             SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
             bar_top = 0;
             return fail(SHP_ERR_HIP, "llama: persistent decode grid barrier timed out; state "
@@ -220,6 +224,12 @@ struct Llama {
         SHP_HIP_CHECK(hipMalloc((void**)&cand, (size_t)p_grid * sizeof(ArgmaxCand)));
         allocs.push_back(cand);
         pa.cand = cand;
+        unsigned long long* tag = nullptr;
+        const size_t tbytes = (size_t)qkv_rows() * sizeof(unsigned long long);
+        SHP_HIP_CHECK(hipMalloc((void**)&tag, tbytes));
+        allocs.push_back(tag);
+        SHP_HIP_CHECK(hipMemset(tag, 0, tbytes));  // epoch 0: never a live phase's
+        pa.qkv_tag = tag;
         const size_t fbytes = persist_flag_slots(p_grid) * sizeof(unsigned long long);
         SHP_HIP_CHECK(hipMalloc((void**)&bar, fbytes));
         allocs.push_back(bar);
