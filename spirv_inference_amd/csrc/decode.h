@@ -64,6 +64,7 @@ struct PersistArgs {
     // [(n_heads + 2 n_kv) * 64] the qkv rows as tagged words, (phase epoch << 32) | float bits:
     // attention waits for its head's words instead of a grid barrier
     unsigned long long* qkv_tag;
+    unsigned long long* x_tag;  // [hidden] x as tagged words (the phases that write x tag it)
     float* att;     // [n_heads * 64] attention output
     float* act;     // [ffn] silu(gate) * up
     float* logits;  // [vocab]

@@ -23,6 +23,14 @@
 // argmax, then F the global argmax (every workgroup reduces the candidates itself).
 // Layer 0 reads the embedding row directly, so no barrier is needed between tokens.
 //
+// Grid barriers follow B1, C, D and E.  A and B2 end without one: their outputs are also
+// stored as tagged words, (phase epoch << 32) | float bits, in one 64-bit store each, and
+// their only consumers (attention for A's q / k / v, the gate/up norm for B2's x) poll
+// exactly the words they need until every tag carries the phase's epoch.  That saves the
+// producer's wait for its stores, the flag round trip and the separate data load.  The
+// write-after-read hazards those barriers also covered stay covered: the next writes of qkv
+// and x come after the following grid barrier.
+//
 // Weight rows are streamed with 16-byte non-temporal loads, up to three chunks (64 KB each per
 // CU) ahead of the arithmetic, on a schedule that keeps each CU's load pipe (~30 GB/s, ~64 KB
 // in flight) busy through the short latency-bound phases (see the layer loop).  The
@@ -202,8 +210,8 @@ struct Epi {
     int row0;
     float best;          // EPI_LOGITS: this wavefront's running max / index
     int best_idx;
-    unsigned long long* tag;  // EPI_QKV: tagged copy of each row, (epoch << 32) | float bits
-    unsigned epoch;
+    unsigned long long* tag;  // EPI_QKV, EPI_RESID: tagged copy of each row,
+    unsigned epoch;           // (epoch << 32) | float bits
 };
 
 // A row is complete: its total (in every lane), then the epilogue (lane 0 stores).
@@ -222,7 +230,13 @@ __device__ __forceinline__ void row_done(float part, int row, int r1, Epi& e) {
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     } else if constexpr (EPI == EPI_RESID) {
-        if (l0) st_coh(e.out + row, s + e.resid[row]);
+        if (l0) {
+            const float v = s + e.resid[row];
+            st_coh(e.out + row, v);
+            __hip_atomic_store((SHP_GLOBAL unsigned long long*)(e.tag + row),
+                               ((unsigned long long)e.epoch << 32) | __float_as_uint(v),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     } else if constexpr (EPI == EPI_SWIGLU) {
         if (l0) e.rows[row - e.row0] = s;
     } else {
@@ -393,6 +407,54 @@ __device__ __forceinline__ NormIn norm_load(const float* __restrict__ x, bool co
     }
     return r;
 }
+// norm_load for x written by the phase with epoch `epoch`: this thread's four tagged words
+// are polled until all carry it (bounded like the barriers; okw[wave] = 0 when a wait gave
+// up).  The caller issues its prefetch loads first, so the first poll returns after them.
+__device__ __forceinline__ NormIn norm_load_tagged(const PersistArgs& a, unsigned epoch, int K,
+                                                   const float* __restrict__ w, int* okw) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const bool act = t < K / 4;
+    NormIn r;
+    r.w = act ? ldg4(w + 4 * t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)a.x_tag + 4 * t;
+    unsigned long long v[4] = {0, 0, 0, 0};
+    int ok = 1;
+    long long n = 0;
+    while (true) {
+        bool ready = true;
+        if (act) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = __hip_atomic_load(q + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ready = ready && (unsigned)(v[i] >> 32) == epoch;
+            }
+        }
+        if (__all(ready)) break;
+        __builtin_amdgcn_s_sleep(1);
+        if ((++n & 127) == 0) {
+            if (__hip_atomic_load((SHP_GLOBAL int*)a.abort_flag, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                n > a.spin_limit) {
+                if (lane == 0)
+                    __hip_atomic_store((SHP_GLOBAL int*)a.abort_flag, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+        }
+    }
+    if (lane == 0) okw[wave] = ok;
+    r.x = make_float4(__uint_as_float((unsigned)v[0]), __uint_as_float((unsigned)v[1]),
+                      __uint_as_float((unsigned)v[2]), __uint_as_float((unsigned)v[3]));
+    return r;
+}
+__device__ __forceinline__ bool all_ok(const int* okw) {
+    int all = 1;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) all &= okw[w];
+    return all != 0;
+}
+
 __device__ __forceinline__ void norm_finish(NormIn in, int K, float eps, float* scratch,
                                             float* xs, float4* xn) {
     const int t = threadIdx.x;
@@ -719,18 +781,20 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                 __syncthreads();
                 e.out = a.x;
                 e.resid = xs;
+                e.tag = a.x_tag;
+                e.epoch = (unsigned)(target + 1);
                 row_done<EPI_RESID>(chunk_dot(b2, xn), h0 + wave_id(), h1, e);
             }
+            // No grid barrier: the gate/up phase waits for the tagged x words.
             stamp(a, it, kb, 0);
-            bar_arrive(a.flags, target + 1);
             load_chunk(b2, L.w_gu, H4, 2 * p0 + 8 * (nls + 2), 0, 2 * p1, a.zero_row);
             target += 1;
-            if (!bar_wait(a, target, okw)) return;
             stamp(a, it, kb++, 1);
             // ---- C: gate/up + SwiGLU ------------------------------------------------------
             {
-                NormIn xr = norm_load(a.x, true, H, L.ffn_norm);
+                NormIn xr = norm_load_tagged(a, (unsigned)target, H, L.ffn_norm, okw);
                 norm_finish(xr, H, a.eps, scratch, xs, xn);
+                if (!all_ok(okw)) return;
                 e.rows = gu_rows;
                 e.row0 = 2 * p0;
                 stream_rows_staged<EPI_SWIGLU>(L.w_gu, H4, 2 * p0, 2 * p1, nls, stage, xn, b0, b1,
@@ -758,6 +822,8 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
                 __syncthreads();
                 e.out = a.x;
                 e.resid = xs;
+                e.tag = a.x_tag;
+                e.epoch = (unsigned)(target + 1);
                 // one row group (h1 - h0 <= 8): JF segment chunks, summed in segment order
                 if constexpr (JF <= 3) {
                     if constexpr (JF == 3) load_chunk(b2, L.w_down, F4, h0, 2, h1, a.zero_row);

@@ -130,6 +130,9 @@ struct Llama {
             SHP_HIP_CHECK(hipMemsetAsync(pa.qkv_tag, 0,
                                          (size_t)qkv_rows() * sizeof(unsigned long long),
                                          ctx->stream));
+            SHP_HIP_CHECK(hipMemsetAsync(pa.x_tag, 0,
+                                         (size_t)cfg.hidden * sizeof(unsigned long long),
+                                         ctx->stream));
             SHP_HIP_CHECK(hipStreamSynchronize(ctx->stream));
             bar_top = 0;
             return fail(SHP_ERR_HIP, "llama: persistent decode grid barrier timed out; state "
@@ -230,6 +233,12 @@ struct Llama {
         allocs.push_back(tag);
         SHP_HIP_CHECK(hipMemset(tag, 0, tbytes));  // epoch 0: never a live phase's
         pa.qkv_tag = tag;
+        unsigned long long* xtag = nullptr;
+        const size_t xbytes = (size_t)cfg.hidden * sizeof(unsigned long long);
+        SHP_HIP_CHECK(hipMalloc((void**)&xtag, xbytes));
+        allocs.push_back(xtag);
+        SHP_HIP_CHECK(hipMemset(xtag, 0, xbytes));
+        pa.x_tag = xtag;
         const size_t fbytes = persist_flag_slots(p_grid) * sizeof(unsigned long long);
         SHP_HIP_CHECK(hipMalloc((void**)&bar, fbytes));
         allocs.push_back(bar);
