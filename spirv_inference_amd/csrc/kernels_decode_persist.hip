@@ -498,38 +498,12 @@ __device__ __forceinline__ float lane_bcast(float v, int src) {
 // through LDS to all 8 wavefronts, which split the PV sum.  The current position comes last,
 // from the rotated k / v; the workgroup of the group's first query head appends those to
 // the cache.  kv_s: [64][KSTRIDE] K | [64][64] V | q, k, v [3][64] | p [64] | PV [NW][64].
-// Tile 0 (cached positions 0 .. min(64, pos) - 1) of the K / V rows of query head h's KV group
-// into kv_s, as attention_heads stages it.  Those rows were written by earlier tokens, so this
-// can run before the qkv barrier's wait.
-__device__ __forceinline__ void stage_kv_tile0(const PersistArgs& a, int l, int pos, int h,
-                                               float* kv_s) {
-    const int t = threadIdx.x;
-    const int nkv = a.n_kv, grp = a.n_heads / nkv, S = a.max_seq, g = h / grp;
-    const int64_t per_layer = (int64_t)nkv * S * 64;
-    const float* kg = a.k_cache + l * per_layer + (int64_t)g * S * 64;
-    const float* vg = a.v_cache + l * per_layer + (int64_t)g * S * 64;
-    float* ks = kv_s;
-    float* vs = ks + 64 * KSTRIDE;
-    const int nrows = min(64, pos);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int f = t + NT * u, row = f >> 4, c4 = f & 15;
-        if (row < nrows) {
-            const unsigned off = (unsigned)(row * 64 + c4 * 4) * 4u;
-            const float4 k = ld_coh4_at(kg, off), v = ld_coh4_at(vg, off);
-            *reinterpret_cast<float4*>(ks + row * KSTRIDE + c4 * 4) = k;
-            *reinterpret_cast<float4*>(vs + row * 64 + c4 * 4) = v;
-        }
-    }
-}
-
-// pre: tile 0 of the first head (h = blockIdx.x) is already in kv_s (stage_kv_tile0, followed
-// by a workgroup barrier).  q, k and v of the current position are read from a.qkv_tag once
+// q, k and v of the current position are read from a.qkv_tag once
 // all 192 words carry `epoch` (the qkv phase's); false (uniformly over the workgroup) when that
 // wait gave up or another workgroup did.  okw: NW ints of LDS.
 __device__ __forceinline__ bool attention_heads(const PersistArgs& a, int l, int pos,
-                                                float* kv_s, int it, int kb, bool pre,
-                                                unsigned epoch, int* okw) {
+                                                float* kv_s, int it, int kb, unsigned epoch,
+                                                int* okw) {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int nq = a.n_heads, nkv = a.n_kv, grp = nq / nkv, S = a.max_seq;
     const int64_t per_layer = (int64_t)nkv * S * 64;
@@ -553,12 +527,11 @@ __device__ __forceinline__ bool attention_heads(const PersistArgs& a, int l, int
         float qr = 0.0f, kr = 0.0f, vcur = 0.0f, o = 0.0f, m = -FLT_MAX, lsum = 0.0f;
         for (int t0 = 0;; t0 += 64) {
             const int nrows = min(64, pos - t0);  // cached rows in this tile (<= 0: none)
-            const bool staged = pre && t0 == 0 && h == (int)blockIdx.x;
             float4 k4[2], v4[2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int f = t + NT * u, row = f >> 4, c4 = f & 15;
-                if (row < nrows && !staged) {
+                if (row < nrows) {
                     const unsigned off = (unsigned)((t0 + row) * 64 + c4 * 4) * 4u;
                     k4[u] = ld_coh4_at(kg, off);
                     v4[u] = ld_coh4_at(vg, off);
@@ -595,7 +568,7 @@ __device__ __forceinline__ bool attention_heads(const PersistArgs& a, int l, int
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int f = t + NT * u, row = f >> 4, c4 = f & 15;
-                if (row < nrows && !staged) {
+                if (row < nrows) {
                     *reinterpret_cast<float4*>(ks + row * KSTRIDE + c4 * 4) = k4[u];
                     *reinterpret_cast<float4*>(vs + row * 64 + c4 * 4) = v4[u];
                 }
@@ -747,19 +720,14 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             // No grid barrier after the qkv phase: only attention consumes qkv, and it waits for
             // the tagged words of its head (the phase's epoch is used for the tags alone).
             stamp(a, it, kb, 0);
-            // The workgroups with one attention head stage its cached K / V tile first (the
-            // tag poll would wait for those loads anyway).
-            const bool pre_kv = attn_wg && G >= a.n_heads;
             if (!attn_wg) {
                 load_chunk(b0, L.w_gu, H4, 2 * p0, 0, 2 * p1, a.zero_row);
                 load_chunk(b1, L.w_gu, H4, 2 * p0 + 8, 0, 2 * p1, a.zero_row);
-            } else if (pre_kv) {
-                stage_kv_tile0(a, l, pos, b, kv_s);
             }
             target += 1;
             stamp(a, it, kb++, 1);
             // ---- B1: attention, one workgroup per query head ------------------------------
-            if (attn_wg && !attention_heads(a, l, pos, kv_s, it, kb, pre_kv, (unsigned)target, okw))
+            if (attn_wg && !attention_heads(a, l, pos, kv_s, it, kb, (unsigned)target, okw))
                 return;
             stamp(a, it, kb, 0);
             bar_arrive(a.flags, target + 1);
