@@ -7,9 +7,9 @@
 // Why one launch: at batch 1 a token is ~115 small HBM-bound GEMVs.  As separate kernels each
 // pays a launch gap, a ramp and a drain, and those dominate the 2-90 MB reads.  Here one
 // workgroup of 512 threads runs on every CU for the whole call; the phases of a layer are
-// separated by grid barriers (an arrival counter in device memory), and before waiting at a
-// barrier every workgroup already issues the weight loads of its share of the NEXT phase
-// (weights do not depend on the barrier), so HBM keeps streaming while the grid synchronises.
+// separated by grid barriers (per-workgroup epoch flags) or tagged-word waits, and before
+// waiting every workgroup already issues the weight loads of its share of the NEXT phase
+// (weights do not depend on the wait), so HBM keeps streaming while the grid synchronises.
 //
 // Phases of one layer (rows of each matrix split evenly over the workgroups):
 //   A  qkv = Wqkv . rmsnorm(x) * attn_norm
@@ -699,12 +699,13 @@ __global__ __launch_bounds__(NT, 1) void decode_persistent_kernel(PersistArgs a)
             const float* xin = l == 0 ? erow : a.x;
             Epi e{};
             // Prefetch schedule.  A CU streams ~30 GB/s with ~64 KB in flight; loads return in
-            // issue order, so a load issued before a barrier delays that barrier's poll.  The
-            // pipe is kept busy through the short phases: qkv chunks 0-1 at the previous
-            // barrier, Wo at the start of the qkv phase, gate/up 0-1 at the qkv barrier (or,
-            // for the workgroups that compute attention, after it), on the others gate/up 0-1
+            // issue order, so a load issued before a wait delays that wait's poll, and a load
+            // issued before a phase's stores delays its barrier arrival.  The pipe is kept busy
+            // through the short phases: qkv chunks 0-1 at the previous barrier, Wo at the
+            // start of the qkv phase, gate/up 0-1 at the end of the qkv phase (or, for the
+            // workgroups that compute attention, after attention), on the others gate/up 0-1
             // moved to LDS and 2-3 issued at the attention barrier, the next gate/up chunk at
-            // the Wo barrier, down 0-1 at the gate/up barrier.
+            // the end of the Wo phase, down 0-1 at the gate/up barrier.
             // ---- A: qkv (at most two chunks, both resident) -------------------------------
             {
                 NormIn xr = norm_load(xin, l != 0, H, L.attn_norm);
