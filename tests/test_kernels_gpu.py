@@ -288,6 +288,38 @@ def test_depthwise_nhwc_lds_tiles(ctx, orc, k, s, dil, c, n, h, w):
     np.testing.assert_array_equal(ys[1], ys[-1])
 
 
+@pytest.mark.parametrize("k,s,c,n,h,w", [(3, 1, 20, 2, 15, 13), (5, 2, 100, 3, 17, 30),
+                                         (5, 1, 8, 1, 9, 11), (3, 2, 36, 1, 7, 7),
+                                         (5, 1, 240, 2, 28, 28)])
+def test_depthwise_nhwc_wblocked(ctx, orc, k, s, c, n, h, w):
+    """The W-blocked NHWC kernel (4 outputs per thread along W) on output widths that are not
+    multiples of 4, stride 1 and 2, 3x3 and 5x5, with residual + ReLU6: against the oracle,
+    bit for bit against the fixed-size kernel, and the automatic choice (the W-blocked kernel
+    for 5x5 with output width >= 14) bit for bit the same."""
+    from spirv_inference_amd._lib import check, lib
+    oh, ow = -(-h // s), -(-w // s)
+    pt = max((oh - 1) * s + k - h, 0) // 2
+    pl = max((ow - 1) * s + k - w, 0) // 2
+    total = n * oh * ow * c
+    push = [n, c, h, w, oh, ow, k, k, s, s, 1, pt, pl, 1, 1, total]
+    x = rnd(n, h, w, c)
+    wt = np.concatenate([rnd(k * k * c, scale=0.3), rnd(c)])
+    res = rnd(total)
+    r = orc.run("depthwise_conv2d_nhwc", x, wt, total, push, residual=res, act="relu6")
+    ys = {}
+    try:
+        for mode in (2, -1, 0):  # forced W-blocked / fixed, automatic
+            check(lib().shp_tune(ctx.handle, b"dw_tile", mode), "tune")
+            ys[mode] = hip(ctx, "depthwise_conv2d_nhwc", x, wt, total, push, residual=res,
+                           act="relu6")
+    finally:
+        check(lib().shp_tune(ctx.handle, b"dw_tile", 0), "tune")
+    assert_close(ys[2], r, 1e-4, 1e-4, "dw nhwc W-blocked")
+    np.testing.assert_array_equal(ys[2], ys[-1])
+    if k == 5 and ow >= 14:
+        np.testing.assert_array_equal(ys[0], ys[2])
+
+
 def test_resize_bilinear(ctx, orc):
     x = rnd(2, 3, 17, 13)
     for ac, hp in [(1, 0), (0, 1), (0, 0)]:
