@@ -1801,12 +1801,13 @@ double plan_cost(const GemmParams& p, int nbatch, TileCfg t, int splits, int kps
     return cost;
 }
 
-// Plans measured best on MI355X for the benchmark configs' shapes (sweeps of every tile, K
-// tile and split count of both kernels per shape; an entry only where the best plan beat the
-// cost model's by more than 2.5 % alone and did not lose inside the model's forward pass,
-// measured op by op with the two plans interleaved); the cost model decides every other shape.  Key: operand
-// modes, batch count, M, N, K, and for convolutions the input channels, stride and kernel
-// height (0 for products).
+// Plans measured best on MI355X for the benchmark configs' shapes: sweeps of every tile, K
+// tile and split count of both kernels per shape, with split counts down to one K tile per
+// split for the 1x1 convolutions of MobileNetV2 b1 and EfficientNet-Lite0 b8.  An entry only
+// where the best plan beat the cost model's by more than 2.5 % alone and did not lose inside
+// the model's forward pass; the cost model decides every other shape.  Key: operand modes,
+// batch count, M, N, K, and for convolutions the input channels, stride and kernel height (0
+// for products).
 struct TunedPlan {
     int amode, bmode, nbatch, M, N, K, cic, csh, ckh;
     TileCfg t;
@@ -1827,8 +1828,8 @@ const TunedPlan kTuned[] = {
     {shp::A_CONV_NHWC, shp::B_STRIDED, 1, 100352, 32, 27, 3, 2, 3, {64, 64, 32, false, 1, false}, 1},  // efficientnet_lite0 stem: 21.4 vs 22.2 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 100352, 96, 16, 16, 1, 1, {64, 64, 16, false, 1, true}, 1},  // efficientnet_lite0 block1_expand: 19.2 vs 19.7 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 6272, 240, 40, 40, 1, 1, {64, 64, 16, false, 1, false}, 1},  // efficientnet_lite0 block4_expand: 10.6 vs 11.5 us
-    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 1568, 80, 480, 480, 1, 1, {64, 64, 32, false, 1, true}, 2},  // efficientnet_lite0 block6_project: 15.3 vs 16.8 us
-    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 1568, 112, 480, 480, 1, 1, {64, 64, 32, false, 1, true}, 1},  // efficientnet_lite0 block8_project: 15.0 vs 16.3 us
+    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 1568, 80, 480, 480, 1, 1, {64, 64, 16, false, 1, true}, 5},  // efficientnet_lite0 block6_project: 12.2 vs 15.3 us
+    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 1568, 112, 480, 480, 1, 1, {64, 64, 16, false, 1, true}, 5},  // efficientnet_lite0 block8_project: 12.8 vs 15.0 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 1568, 672, 112, 112, 1, 1, {64, 64, 16, false, 1, true}, 1},  // efficientnet_lite0 block9_expand: 11.2 vs 11.5 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 392, 1152, 192, 192, 1, 1, {64, 64, 32, false, 1, true}, 1},  // efficientnet_lite0 block12_expand: 10.5 vs 11.1 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 392, 192, 1152, 1152, 1, 1, {64, 64, 16, false, 1, true}, 6},  // efficientnet_lite0 block12_project: 13.6 vs 13.9 us
@@ -1839,15 +1840,15 @@ const TunedPlan kTuned[] = {
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 3136, 24, 96, 96, 1, 1, {64, 64, 16, false, 1, true}, 1},  // mobilenet_v2 block1_project: 8.4 vs 8.7 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 64, 192, 192, 1, 1, {64, 64, 16, false, 1, true}, 1},  // mobilenet_v2 block6_project: 10.0 vs 10.7 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 384, 64, 64, 1, 1, {64, 64, 16, false, 1, true}, 1},  // mobilenet_v2 block7_expand: 7.8 vs 8.4 us
-    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 64, 384, 384, 1, 1, {64, 64, 32, false, 1, true}, 1},  // mobilenet_v2 block7_project: 13.5 vs 14.4 us
-    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 96, 384, 384, 1, 1, {64, 64, 32, false, 1, true}, 1},  // mobilenet_v2 block10_project: 13.2 vs 14.2 us
+    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 64, 384, 384, 1, 1, {64, 64, 32, false, 1, true}, 6},  // mobilenet_v2 block7_project: 11.0 vs 13.6 us
+    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 96, 384, 384, 1, 1, {64, 64, 16, false, 1, true}, 6},  // mobilenet_v2 block10_project: 10.6 vs 13.4 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 576, 96, 96, 1, 1, {64, 64, 16, false, 1, true}, 1},  // mobilenet_v2 block11_expand: 8.5 vs 9.0 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 196, 96, 576, 576, 1, 1, {64, 64, 32, false, 1, true}, 5},  // mobilenet_v2 block11_project: 11.7 vs 12.3 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 160, 576, 576, 1, 1, {64, 64, 16, false, 1, true}, 5},  // mobilenet_v2 block13_project: 11.7 vs 12.2 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 960, 160, 160, 1, 1, {64, 64, 16, false, 1, true}, 1},  // mobilenet_v2 block14_expand: 9.5 vs 9.9 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 160, 960, 960, 1, 1, {64, 64, 16, false, 1, true}, 8},  // mobilenet_v2 block14_project: 12.4 vs 14.1 us
     {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 320, 960, 960, 1, 1, {64, 64, 16, false, 1, true}, 6},  // mobilenet_v2 block16_project: 12.4 vs 13.0 us
-    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 1280, 320, 320, 1, 1, {64, 64, 32, false, 1, true}, 1},  // mobilenet_v2 head_conv: 12.2 vs 14.7 us
+    {shp::A_CONV_NHWC4, shp::B_KVEC, 1, 49, 1280, 320, 320, 1, 1, {64, 64, 16, false, 1, true}, 5},  // mobilenet_v2 head_conv: 10.8 vs 12.3 us
 };
 
 // The table's plan for this problem, if it has one that the problem's operands allow.
@@ -1891,7 +1892,8 @@ bool plan_bl(const GemmParams& p, int nbatch, int blm, const shp::GemmTune& tn, 
             if (tn.splits && tn.splits != s) continue;
             int kps = ((p.K + s - 1) / s + kq - 1) / kq * kq;
             int real = (p.K + kps - 1) / kps;
-            if (s > 1 && (real != s || kps < 128)) continue;
+            // the model keeps 128 K per split; a forced split count may go down to one K tile
+            if (s > 1 && (real != s || kps < (tn.splits ? kq : 128))) continue;
             double c = plan_cost(p, nbatch, t, s, kps);
             if (c < best_cost * 0.97) {
                 best_cost = c;
