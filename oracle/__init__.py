@@ -6,6 +6,7 @@ cpu_baseline leg, always as the checker or the CPU baseline, never as the produc
 from __future__ import annotations
 
 import ctypes as C
+import os
 import pathlib
 import subprocess
 from typing import Optional, Sequence
@@ -13,7 +14,8 @@ from typing import Optional, Sequence
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# SHP_ORACLE_LIB selects another build of the same source (the sanitizer build of `make asan`)
+LIB_PATH = pathlib.Path(os.environ.get("SHP_ORACLE_LIB", HERE / "liboracle.so"))
 _LIB = None
 
 ACT = {"none": 0, "relu": 1, "relu6": 2, "leaky": 3, "sigmoid": 4, "tanh": 5, "silu": 6,

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close
+from conftest import assert_close, ulp_diff
 
 RNG = np.random.default_rng(1234)
 
@@ -313,3 +313,67 @@ def test_gather_rows_vs_numpy_take(orc):
     ok = (ids >= 0) & (ids < rows)
     assert y[ok].tobytes() == np.take(table, ids[ok], axis=0).tobytes()
     assert not y[~ok].any()
+
+
+def _rounding_probe_inputs():
+    """Inputs that separate floor/ceil/sin/cos from plausible mistakes: a dense random sweep
+    over +-1e4, exact integers and half-integers, +-0, the float32 neighbours just below and
+    above integers, and large magnitudes where sin's argument reduction and the 2^23 limit
+    (every float32 at or above it is an integer) matter."""
+    rng = np.random.default_rng(77)
+    sweep = rng.uniform(-1e4, 1e4, 100_000)
+    ints = np.arange(-1000, 1001, dtype=np.float64)
+    halves = ints + 0.5
+    f_ints = ints.astype(np.float32)
+    below = np.nextafter(f_ints, np.float32(-np.inf))
+    above = np.nextafter(f_ints, np.float32(np.inf))
+    big = np.concatenate([2.0 ** np.arange(20, 100), -(2.0 ** np.arange(20, 100)),
+                          rng.uniform(1e5, 1e30, 2000) * rng.choice([-1, 1], 2000),
+                          [8388607.5, -8388607.5, 8388608.0, 16777217.0, 3.4e38, -3.4e38]])
+    # multiples of pi/2 in float32: sin/cos results near zero, where a wrong reduction fails
+    near_pi = (np.arange(-2000, 2001) * (np.pi / 2)).astype(np.float32)
+    return np.concatenate([sweep.astype(np.float32), f_ints, halves.astype(np.float32), below,
+                           above, np.float32([0.0, -0.0, 1e-45, -1e-45, 1e-30, -1e-30]),
+                           big.astype(np.float32), near_pi]).astype(np.float32)
+
+
+@pytest.mark.parametrize("name,ref", [("floor", np.floor), ("ceil", np.ceil)])
+def test_floor_ceil_bit_exact_vs_float64(orc, name, ref):
+    """floor/ceil (`compiler.rs:1495-1499` f32::floor/ceil in cpu_elementwise) are exact in
+    float32: the float64 result of a float32 input is representable, so the oracle must equal
+    it bit for bit, signed zeros included (ceil(-0.5) = -0.0)."""
+    x = _rounding_probe_inputs()
+    y = orc.run(name, x, None, x.size, [x.size])
+    want = ref(x.astype(np.float64)).astype(np.float32)
+    assert y.tobytes() == want.tobytes(), name
+    # signed zero and infinity handling spelled out
+    s = orc.run(name, np.float32([-0.5, 0.5, -0.0, np.inf, -np.inf]), None, 5, [5])
+    exp = {"floor": [-1.0, 0.0, -0.0, np.inf, -np.inf], "ceil": [-0.0, 1.0, -0.0, np.inf, -np.inf]}
+    assert s.tobytes() == np.float32(exp[name]).tobytes()
+
+
+@pytest.mark.parametrize("name,ref", [("sine", np.sin), ("cosine", np.cos)])
+def test_sin_cos_within_one_ulp_of_float64(orc, name, ref):
+    """sine (`kernels/sine/glsl/sine.comp:10`, o[i] = sin(a[i])) and the HLO path's
+    f32::sin/cos (`compiler.rs:1495-1499`) against float64 numpy of the same float32 input:
+    at most 1 ULP of the correctly rounded result everywhere, including the float32 multiples
+    of pi/2 (results near zero) and magnitudes up to 3.4e38 (full argument reduction).  A
+    reduction done in float32, a swapped sin/cos or a dropped sign fails this by many ULP."""
+    x = _rounding_probe_inputs()
+    y = orc.run(name, x, None, x.size, [x.size])
+    exact = ref(x.astype(np.float64))
+    want = exact.astype(np.float32)
+    assert ulp_diff(y, want).max() <= 1, f"{name}: max ulp {ulp_diff(y, want).max()}"
+    # identities that fix the sign and the phase: sin(-x) = -sin(x), cos(-x) = cos(x)
+    yn = orc.run(name, -x, None, x.size, [x.size])
+    if name == "sine":
+        assert yn.tobytes() == (-y).tobytes()
+    else:
+        assert yn.tobytes() == y.tobytes()
+    # special values: sin(+-0) keeps the sign, cos(0) = 1, non-finite inputs give NaN
+    sp = orc.run(name, np.float32([0.0, -0.0, np.inf, -np.inf, np.nan]), None, 5, [5])
+    if name == "sine":
+        assert sp[:2].tobytes() == np.float32([0.0, -0.0]).tobytes()
+    else:
+        assert (sp[:2] == 1.0).all()
+    assert np.isnan(sp[2:]).all()
