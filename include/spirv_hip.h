@@ -161,6 +161,11 @@ int shp_timing_reset(shp_ctx* ctx);
 /* Fills name/total ms/count of entry `index` (synchronises first). */
 int shp_timing_entry(shp_ctx* ctx, int index, char* name, size_t name_cap, double* total_ms,
                      uint64_t* count);
+/* The timed launches one by one, in issue order since the last reset: the per-dispatch
+ * `elapsed_ms` of the HLO runner's report (source/xla_hlo/src/compiler.rs:675-692
+ * dispatch_record).  Both synchronise first. */
+int shp_timing_launch_count(shp_ctx* ctx, uint64_t* count);
+int shp_timing_launch(shp_ctx* ctx, uint64_t index, char* name, size_t name_cap, double* ms);
 
 /* ---- resident op graphs: the chained runtime (runtime/chained_graph_runtime/src/main.rs:260-590)
  *      generalised, and the model drivers of the benchmark configs ---------------- */
@@ -213,7 +218,9 @@ typedef struct shp_llama_config {
 int shp_llama_create(shp_ctx* ctx, const shp_llama_config* cfg, uint64_t seed,
                      shp_llama** out);
 void shp_llama_destroy(shp_llama* lm);
-/* Clears the KV cache and the position counter. */
+/* Clears the KV cache and the position counter.  Like every call below that copies,
+ * clears memory or synchronises, it returns SHP_ERR_INVALID while the context stream is
+ * being captured (between shp_capture_begin and shp_capture_end). */
 int shp_llama_reset(shp_llama* lm);
 /* Runs one token at the current position (KV cache append), writes logits to the
  * device logits buffer and the greedy argmax (lowest index on ties) to the device
@@ -242,6 +249,13 @@ int shp_llama_use_graph(shp_llama* lm, int enable);
 enum { SHP_LLAMA_KERNELS = 0, SHP_LLAMA_GRAPH = 1, SHP_LLAMA_PERSISTENT = 2 };
 int shp_llama_set_engine(shp_llama* lm, int engine);
 int shp_llama_engine(shp_llama* lm, int* engine);
+/* Bound of the persistent engine's grid waits, in polls (default 2^22, about seconds; a
+ * negative value restores it).  A wait that gives up makes every workgroup exit; the call
+ * then returns SHP_ERR_HIP and the decode state is undefined until shp_llama_reset, as
+ * run_llama_spirv.py:76-81,237-246 aborts on a non-zero status.  A small limit forces that
+ * path from the host (tests of the recovery).  No counterpart in the reference, whose
+ * dispatches never wait on each other inside a launch. */
+int shp_llama_set_wait_limit(shp_llama* lm, int64_t polls);
 int shp_llama_logits(shp_llama* lm, void** dptr, uint64_t* elems);
 /* Weight tensors for checkers: which = "embed" [vocab,hidden], "final_norm", "lm_head"
  * [vocab,hidden], or per layer "attn_norm", "wqkv" (rows q | k | v), "wo", "ffn_norm",

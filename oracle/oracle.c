@@ -714,7 +714,7 @@ static const char* kNames[] = {
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
     "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
     "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
-    "hlo_reduce", "hlo_strided_copy", "attention_fused"};
+    "hlo_reduce", "hlo_strided_copy", "attention_fused", "nan_count"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -967,6 +967,22 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
             out[n] = acc;
         }
         epilogue(out, n_out, 0, bias, residual, act, alpha);
+        return 0;
+    }
+    if (!strcmp(name, "nan_count")) {
+        /* compiler.rs:613-623 NaN trace: count of NaN values and the first one's index
+         * (-1 when none), stored as uint32 / int32 bits in out[0], out[1] */
+        NEED(1);
+        TOTAL(2);
+        uint32_t cnt = 0;
+        int32_t first = -1;
+        for (int64_t i = 0; i < (int64_t)push[0]; ++i)
+            if (isnan(in0[i])) {
+                if (first < 0) first = (int32_t)i;
+                ++cnt;
+            }
+        memcpy(&out[0], &cnt, 4);
+        memcpy(&out[1], &first, 4);
         return 0;
     }
     if (!strcmp(name, "gather_rows")) { /* embed_table[ids] (run_llama_spirv.py:203) */

@@ -22,6 +22,8 @@ ERRORS = {
     -7: "SHP_ERR_UNSUPPORTED",
 }
 
+globals().update({name: code for code, name in ERRORS.items()})  # SHP_ERR_* constants
+
 ACT = {"none": 0, "relu": 1, "relu6": 2, "leaky": 3, "sigmoid": 4, "tanh": 5, "silu": 6,
        "gelu_erf": 7}
 
@@ -95,6 +97,9 @@ SIGNATURES = [
     ("shp_timing_reset", C.c_int, [C.c_void_p]),
     ("shp_timing_entry", C.c_int, [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t,
                                    C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    ("shp_timing_launch_count", C.c_int, [C.c_void_p, C.POINTER(C.c_uint64)]),
+    ("shp_timing_launch", C.c_int, [C.c_void_p, C.c_uint64, C.c_char_p, C.c_size_t,
+                                    C.POINTER(C.c_double)]),
     ("shp_model_create", C.c_int, [C.c_void_p, C.c_char_p, C.c_int32, C.c_int32, C.c_uint64,
                                    C.POINTER(C.c_void_p)]),
     ("shp_model_destroy", None, [C.c_void_p]),
@@ -124,6 +129,7 @@ SIGNATURES = [
                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("shp_llama_use_graph", C.c_int, [C.c_void_p, C.c_int]),
     ("shp_llama_set_engine", C.c_int, [C.c_void_p, C.c_int]),
+    ("shp_llama_set_wait_limit", C.c_int, [C.c_void_p, C.c_int64]),
     ("shp_llama_engine", C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
     ("shp_llama_logits", C.c_int, [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]),
     ("shp_llama_weight", C.c_int, [C.c_void_p, C.c_int32, C.c_char_p, C.POINTER(C.c_void_p),

@@ -162,9 +162,15 @@ def read_npy_f32(path: pathlib.Path) -> np.ndarray:
     return a.reshape(-1)
 
 
-def spv_entry(path: str | None) -> dict:
-    p = pathlib.Path(path) if path else None
-    return {"path": path, "sha256": sha256_bytes(p.read_bytes()) if p and p.is_file() else None}
+def spv_entry(path: str) -> dict:
+    """main.rs:109-120: each --*-spv file is read (and hashed) before anything runs; an
+    unreadable path is an error naming it.  The bytes are not used here (the kernels are
+    compiled into the library), only recorded."""
+    try:
+        data = pathlib.Path(path).read_bytes()
+    except OSError as e:
+        raise OSError(f"reading {path}: {e.strerror or e}") from e
+    return {"path": path, "sha256": sha256_bytes(data)}
 
 
 def main(argv=None) -> int:
@@ -191,6 +197,12 @@ def main(argv=None) -> int:
     if any(v.size != ELEMENTS for v in want.values()):
         raise ValueError("unexpected fixture sizes for 256-element Conv2D -> BatchNorm -> ReLU "
                          "-> Softmax harness")
+    try:
+        source_spv = {k: spv_entry(getattr(a, f"{k}_spv")) for k in
+                      ("conv2d", "batchnorm", "relu", "softmax")}
+    except OSError as e:
+        print(f"error: {e}", file=sys.stderr)
+        return 1
     from .runtime import Context
     a.dump_dir.mkdir(parents=True, exist_ok=True)
     with Context("any" if a.device in ("any", "amd") else a.device) as ctx:
@@ -228,8 +240,7 @@ def main(argv=None) -> int:
             "softmax": {"kernel": L["softmax"][0], "push": L["softmax"][1]},
             "ordering": "one HIP stream: each stage reads the previous edge after it is written",
         },
-        "source_spv": {k: spv_entry(getattr(a, f"{k}_spv")) for k in
-                       ("conv2d", "batchnorm", "relu", "softmax")},
+        "source_spv": source_spv,
         "fixture_manifest": str(a.fixture_manifest),
         "fixture_hashes": {
             **{k: man["inputs"][k].get("sha256") for k in man["inputs"]},

@@ -75,6 +75,7 @@ struct PersistArgs {
     int* abort_flag;            // set when a barrier wait exceeds spin_limit
     unsigned long long bar_base;  // barriers completed before this launch (epoch base)
     long long spin_limit;         // polls of the counter before a wait gives up
+    long long spin_start;         // poll count a wait starts from (0, or 127: check at once)
     int n_layers, hidden, n_heads, n_kv, ffn, vocab, max_seq;
     float eps, theta;
     int n_tokens;      // tokens decoded by this launch

@@ -53,7 +53,9 @@
 // wavefronts poll the flags.  No L2 write-back or invalidate is needed, which is what makes a
 // barrier ~2.5 us instead of ~10-30 us with release/acquire fences on MI355X.
 // Every wait is bounded (spin_limit polls); on expiry the workgroup raises abort_flag and
-// every workgroup exits, so the grid always drains.
+// every workgroup exits, so the grid always drains.  A wait checks the flag and its limit every
+// 128 polls, counting from spin_start (0; 127 makes the first missed poll check already, which
+// lets the host force a give-up with a small limit).
 #include <cfloat>
 
 #include "decode.h"
@@ -358,7 +360,7 @@ __device__ __forceinline__ bool bar_wait(const PersistArgs& a, unsigned long lon
     if (wave * 64 < G) {
         const int f = wave * 64 + lane;
         int ok = 1;
-        long long n = 0;
+        long long n = a.spin_start;
         while (true) {
             const unsigned long long v =
                 f < G ? __hip_atomic_load((SHP_GLOBAL unsigned long long*)(a.flags + 8 * f),
@@ -419,7 +421,7 @@ __device__ __forceinline__ NormIn norm_load_tagged(const PersistArgs& a, unsigne
     SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)a.x_tag + 4 * t;
     unsigned long long v[4] = {0, 0, 0, 0};
     int ok = 1;
-    long long n = 0;
+    long long n = a.spin_start;
     while (true) {
         bool ready = true;
         if (act) {
@@ -543,7 +545,7 @@ __device__ __forceinline__ bool attention_heads(const PersistArgs& a, int l, int
                     const int which = t >> 6, d = t & 63;
                     const int src = (which == 0 ? h : which == 1 ? nq + g : nq + nkv + g) * 64 + d;
                     unsigned long long w = 0;
-                    long long n = 0;
+                    long long n = a.spin_start;
                     while (true) {
                         w = __hip_atomic_load((SHP_GLOBAL unsigned long long*)(a.qkv_tag + src),
                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -581,6 +581,57 @@ int launch_rownorm(const shp::Launch& l) {
     return SHP_OK;
 }
 
+// ---- nan_count: the NaN trace of the HLO runner (compiler.rs:613-623), on the device -------
+// out[0] = number of NaN values among x[0, n) (uint32 bits), out[1] = index of the first one
+// (int32 bits, -1 when there is none).  The first kernel sets out to {0, 0xFFFFFFFF} (a
+// kernel, not a memset, so the pair can sit inside a captured graph); the second folds a
+// grid-stride count and the smallest index per wavefront and merges them with atomics.
+__global__ void nan_count_init_kernel(uint32_t* out) {
+    out[0] = 0u;
+    out[1] = 0xFFFFFFFFu;
+}
+
+__global__ __launch_bounds__(256) void nan_count_kernel(const float* __restrict__ x,
+                                                        uint32_t* out, uint32_t n) {
+    uint32_t cnt = 0, first = 0xFFFFFFFFu;
+    const uint32_t stride = gridDim.x * 256u;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < n; i += stride) {
+        if (__builtin_isnan(x[i])) {
+            ++cnt;
+            first = first < i ? first : i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        cnt += __shfl_xor(cnt, o);
+        uint32_t f = __shfl_xor(first, o);
+        first = first < f ? first : f;
+    }
+    if ((threadIdx.x & 63) == 0 && cnt) {
+        atomicAdd(&out[0], cnt);
+        atomicMin(&out[1], first);
+    }
+}
+
+int launch_nan_count(const shp::Launch& l) {
+    if (l.n_push < 1) return shp::fail(SHP_ERR_PUSH, "nan_count needs {n}");
+    int64_t n = l.push[0];
+    if (n < 0) return shp::fail(SHP_ERR_SHAPE, "nan_count: n < 0");
+    int rc = shp::check_total(l, 2, "nan_count");
+    if (rc) return rc;
+    if (n > 0 && !l.in0) return shp::fail(SHP_ERR_INVALID, "nan_count: input (in0) required");
+    hipLaunchKernelGGL(nan_count_init_kernel, dim3(1), dim3(1), 0, l.stream, (uint32_t*)l.out);
+    SHP_HIP_CHECK(hipGetLastError());
+    if (n > 0) {
+        unsigned g = cap_grid((uint64_t)n, 256);
+        if (g > 2048) g = 2048;
+        hipLaunchKernelGGL(nan_count_kernel, dim3(g), dim3(256), 0, l.stream,
+                           (const float*)l.in0, (uint32_t*)l.out, (uint32_t)n);
+        SHP_HIP_CHECK(hipGetLastError());
+    }
+    return SHP_OK;
+}
+
 }  // namespace
 
 namespace shp {
@@ -598,6 +649,7 @@ KernelEntry kReduceKernels[] = {
     {"softmax_rows", 3, false, launch_softmax_rows},
     {"layernorm_rows", 3, false, launch_rownorm<false>},
     {"rmsnorm_rows", 3, false, launch_rownorm<true>},
+    {"nan_count", 1, false, launch_nan_count},
 };
 const int kReduceKernelCount = sizeof(kReduceKernels) / sizeof(kReduceKernels[0]);
 

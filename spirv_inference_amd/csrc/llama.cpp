@@ -19,6 +19,7 @@
 namespace shp {
 
 struct Llama {
+    static constexpr long long kDefaultSpinLimit = 1ll << 22;
     Ctx* ctx = nullptr;
     shp_llama_config cfg{};
     uint64_t seed = 0;
@@ -210,7 +211,8 @@ struct Llama {
         pa.zero_row = zero;
         pa.st = st;
         pa.abort_flag = abort_flag;
-        pa.spin_limit = 1ll << 22;  // ~1 us per poll: a wait gives up after seconds
+        pa.spin_limit = kDefaultSpinLimit;  // ~1 us per poll: a wait gives up after seconds
+        pa.spin_start = 0;
         pa.n_layers = cfg.n_layers;
         pa.hidden = cfg.hidden;
         pa.n_heads = cfg.n_heads;
@@ -263,6 +265,10 @@ extern "C" {
 
 int shp_llama_create(shp_ctx* ctx, const shp_llama_config* cfg, uint64_t seed, shp_llama** out) {
     if (!ctx || !cfg || !out) return fail(SHP_ERR_INVALID, "shp_llama_create: null argument");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<shp::Ctx*>(ctx)->stream, "shp_llama_create");
+        if (grc) return grc;
+    }
     *out = nullptr;
     const shp_llama_config& c = *cfg;
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
@@ -332,11 +338,19 @@ void shp_llama_destroy(shp_llama* p) {
 
 int shp_llama_reset(shp_llama* p) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_reset: null");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_reset");
+        if (grc) return grc;
+    }
     return reinterpret_cast<Llama*>(p)->reset();
 }
 
 int shp_llama_step(shp_llama* p, int32_t token) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_step: null");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_step");
+        if (grc) return grc;
+    }
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (token < 0 || token >= lm->cfg.vocab) return fail(SHP_ERR_SHAPE, "shp_llama_step: token id");
     if (lm->engine == SHP_LLAMA_PERSISTENT) return lm->persist_run(1, token);
@@ -346,6 +360,10 @@ int shp_llama_step(shp_llama* p, int32_t token) {
 
 int shp_llama_decode(shp_llama* p, int32_t n_steps) {
     if (!p) return fail(SHP_ERR_INVALID, "shp_llama_decode: null");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_decode");
+        if (grc) return grc;
+    }
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (n_steps < 0) return fail(SHP_ERR_INVALID, "shp_llama_decode: n_steps < 0");
     if (n_steps == 0) return SHP_OK;
@@ -359,6 +377,10 @@ int shp_llama_decode(shp_llama* p, int32_t n_steps) {
 
 int shp_llama_tokens(shp_llama* p, int32_t* out, int32_t cap, int32_t* n_out) {
     if (!p || !n_out) return fail(SHP_ERR_INVALID, "shp_llama_tokens: null");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_tokens");
+        if (grc) return grc;
+    }
     Llama* lm = reinterpret_cast<Llama*>(p);
     shp::DecodeState h;
     SHP_HIP_CHECK(hipMemcpyAsync(&h, lm->st, sizeof(h), hipMemcpyDeviceToHost, lm->ctx->stream));
@@ -374,6 +396,10 @@ int shp_llama_generate(shp_llama* p, const int32_t* prompt, int32_t n_prompt, in
                        int32_t* out_tokens, int32_t* n_out) {
     if (!p || (!prompt && n_prompt) || n_prompt <= 0 || n_new < 0 || !n_out)
         return fail(SHP_ERR_INVALID, "shp_llama_generate: bad arguments");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_generate");
+        if (grc) return grc;
+    }
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (n_prompt + n_new - 1 > lm->cfg.max_seq)
         return fail(SHP_ERR_SHAPE, "shp_llama_generate: prompt + new tokens exceed max_seq");
@@ -423,6 +449,10 @@ int shp_llama_profile_persistent(shp_llama* p, int32_t n, unsigned long long* ho
                                  uint64_t cap, int32_t* grid) {
     if (!p || !host_out || !grid || n <= 0)
         return fail(SHP_ERR_INVALID, "shp_llama_profile_persistent: bad arguments");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<Llama*>(p)->ctx->stream, "shp_llama_profile_persistent");
+        if (grc) return grc;
+    }
     Llama* lm = reinterpret_cast<Llama*>(p);
     if (lm->p_grid <= 0) return fail(SHP_ERR_UNSUPPORTED, "persistent engine unavailable");
     const uint64_t need = (uint64_t)n * shp::persist_barriers_per_token(lm->cfg.n_layers) * 16 *
@@ -439,6 +469,16 @@ int shp_llama_profile_persistent(shp_llama* p, int32_t n, unsigned long long* ho
     (void)hipFree(d);
     *grid = lm->p_grid;
     return rc;
+}
+
+int shp_llama_set_wait_limit(shp_llama* p, int64_t polls) {
+    if (!p) return fail(SHP_ERR_INVALID, "shp_llama_set_wait_limit: null");
+    Llama* lm = reinterpret_cast<Llama*>(p);
+    if (polls < 0) polls = shp::Llama::kDefaultSpinLimit;
+    lm->pa.spin_limit = polls;
+    // below one check interval the first missed poll already checks, so the limit holds
+    lm->pa.spin_start = polls < 128 ? 127 : 0;
+    return SHP_OK;
 }
 
 int shp_llama_engine(shp_llama* p, int* engine) {

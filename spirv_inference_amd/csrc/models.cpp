@@ -478,6 +478,11 @@ extern "C" {
 int shp_model_create(shp_ctx* ctx, const char* arch, int32_t batch, int32_t seq_len,
                      uint64_t seed, shp_model** out) {
     if (!ctx || !arch || !out) return fail(SHP_ERR_INVALID, "shp_model_create: null argument");
+    {
+        int grc = shp::refuse_while_capturing(reinterpret_cast<shp::Ctx*>(ctx)->stream,
+                                              "shp_model_create");
+        if (grc) return grc;
+    }
     if (batch <= 0) return fail(SHP_ERR_SHAPE, "shp_model_create: batch must be > 0");
     *out = nullptr;
     Model* m = new Model();
@@ -510,7 +515,12 @@ void shp_model_destroy(shp_model* model) {
 
 int shp_model_run(shp_model* model) {
     if (!model) return fail(SHP_ERR_INVALID, "shp_model_run: null model");
-    return reinterpret_cast<Model*>(model)->run();
+    Model* m = reinterpret_cast<Model*>(model);
+    if (m->use_graph) {  // the model captures its own graph: no nesting in the caller's
+        int rc = shp::refuse_while_capturing(m->ctx->stream, "shp_model_run with a graph");
+        if (rc) return rc;
+    }
+    return m->run();
 }
 
 int shp_model_use_graph(shp_model* model, int enable) {

@@ -80,6 +80,17 @@ int launch_kernel(hipStream_t stream, const char* name, const void* in0, const v
     return e->fn(l);
 }
 
+int refuse_while_capturing(hipStream_t stream, const char* what) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SHP_HIP_CHECK(hipStreamIsCapturing(stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(SHP_ERR_INVALID,
+                    std::string(what) + ": refused while the context stream is being captured "
+                                        "(the call allocates, copies, clears memory or waits "
+                                        "for the stream)");
+    return SHP_OK;
+}
+
 // ---- context ----------------------------------------------------------------------------
 Ctx::~Ctx() {
     for (auto& t : timers) {
@@ -154,6 +165,7 @@ int Ctx::collect_timing() {
         auto& acc = timing_totals[timers[i].name];
         acc.first += ms;
         acc.second += 1;
+        timing_log.emplace_back(timers[i].name, (double)ms);
     }
     timer_used = 0;
     return SHP_OK;
@@ -246,6 +258,10 @@ int shp_free(shp_ctx* ctx, void* dptr) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_free: null ctx");
     if (!dptr) return SHP_OK;
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_free");
+        if (grc) return grc;
+    }
     SHP_HIP_CHECK(hipStreamSynchronize(c->stream));
     SHP_HIP_CHECK(hipFree(dptr));
     return SHP_OK;
@@ -254,6 +270,10 @@ int shp_free(shp_ctx* ctx, void* dptr) {
 int shp_upload(shp_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(SHP_ERR_INVALID, "shp_upload: null");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_upload");
+        if (grc) return grc;
+    }
     if (!bytes) return SHP_OK;
     SHP_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
     SHP_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -263,6 +283,10 @@ int shp_upload(shp_ctx* ctx, void* dst, const void* src, size_t bytes) {
 int shp_download(shp_ctx* ctx, void* dst, const void* src, size_t bytes) {
     if (!ctx || (bytes && (!dst || !src))) return fail(SHP_ERR_INVALID, "shp_download: null");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_download");
+        if (grc) return grc;
+    }
     if (!bytes) return SHP_OK;
     SHP_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
     SHP_HIP_CHECK(hipStreamSynchronize(c->stream));
@@ -271,7 +295,10 @@ int shp_download(shp_ctx* ctx, void* dst, const void* src, size_t bytes) {
 
 int shp_sync(shp_ctx* ctx) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_sync: null ctx");
-    SHP_HIP_CHECK(hipStreamSynchronize(reinterpret_cast<Ctx*>(ctx)->stream));
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    int rc = shp::refuse_while_capturing(c->stream, "shp_sync");
+    if (rc) return rc;
+    SHP_HIP_CHECK(hipStreamSynchronize(c->stream));
     return SHP_OK;
 }
 
@@ -279,7 +306,9 @@ int shp_sync(shp_ctx* ctx) {
 // Grow the context's split-K workspace so forced split counts are not clamped by it.
 int shp_reserve_workspace(shp_ctx* ctx, uint64_t bytes) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_reserve_workspace: null ctx");
-    return reinterpret_cast<Ctx*>(ctx)->ensure_workspace((size_t)bytes);
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    int rc = shp::refuse_while_capturing(c->stream, "shp_reserve_workspace");
+    return rc ? rc : c->ensure_workspace((size_t)bytes);
 }
 
 // Current split-K workspace of the context (its address and size), for lifetime checks.
@@ -353,6 +382,10 @@ int shp_run_kernel(shp_ctx* ctx, const char* kernel, const float* in0, size_t n0
     if ((n0 && !in0) || (n1 && !in1) || (n_out && !out))
         return fail(SHP_ERR_INVALID, "shp_run_kernel: null buffer with non-zero size");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_run_kernel");
+        if (grc) return grc;
+    }
     if (!shp::find_kernel(kernel))
         return fail(SHP_ERR_UNKNOWN_KERNEL,
                     std::string("unknown kernel '") + (kernel ? kernel : "(null)") + "'");
@@ -488,9 +521,14 @@ int shp_timing_enable(shp_ctx* ctx, int enable) {
 int shp_timing_reset(shp_ctx* ctx) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_timing_reset: null ctx");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_timing_reset");
+        if (grc) return grc;
+    }
     SHP_HIP_CHECK(hipStreamSynchronize(c->stream));
     c->timer_used = 0;
     c->timing_totals.clear();
+    c->timing_log.clear();
     return SHP_OK;
 }
 
@@ -498,6 +536,10 @@ int shp_timing_entry(shp_ctx* ctx, int index, char* name, size_t name_cap, doubl
                      uint64_t* count) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_timing_entry: null ctx");
     Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_timing_entry");
+        if (grc) return grc;
+    }
     int rc = c->collect_timing();
     if (rc) return rc;
     if (index < 0 || index >= (int)c->timing_totals.size())
@@ -510,6 +552,39 @@ int shp_timing_entry(shp_ctx* ctx, int index, char* name, size_t name_cap, doubl
     }
     if (total_ms) *total_ms = it->second.first;
     if (count) *count = it->second.second;
+    return SHP_OK;
+}
+
+int shp_timing_launch_count(shp_ctx* ctx, uint64_t* count) {
+    if (!ctx || !count) return fail(SHP_ERR_INVALID, "shp_timing_launch_count: null argument");
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_timing_launch_count");
+        if (grc) return grc;
+    }
+    int rc = c->collect_timing();
+    if (rc) return rc;
+    *count = c->timing_log.size();
+    return SHP_OK;
+}
+
+int shp_timing_launch(shp_ctx* ctx, uint64_t index, char* name, size_t name_cap, double* ms) {
+    if (!ctx) return fail(SHP_ERR_INVALID, "shp_timing_launch: null ctx");
+    Ctx* c = reinterpret_cast<Ctx*>(ctx);
+    {
+        int grc = shp::refuse_while_capturing(c->stream, "shp_timing_launch");
+        if (grc) return grc;
+    }
+    int rc = c->collect_timing();
+    if (rc) return rc;
+    if (index >= c->timing_log.size())
+        return fail(SHP_ERR_INVALID, "shp_timing_launch: index out of range");
+    const auto& e = c->timing_log[index];
+    if (name && name_cap) {
+        std::strncpy(name, e.first.c_str(), name_cap - 1);
+        name[name_cap - 1] = '\0';
+    }
+    if (ms) *ms = e.second;
     return SHP_OK;
 }
 

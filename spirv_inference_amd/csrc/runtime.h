@@ -33,6 +33,8 @@ struct Ctx {
     std::vector<Timer> timers;
     size_t timer_used = 0;
     std::map<std::string, std::pair<double, uint64_t>> timing_totals;
+    // every timed launch in issue order since the last reset: (kernel name, ms)
+    std::vector<std::pair<std::string, double>> timing_log;
 
     ~Ctx();
     int ensure_workspace(size_t bytes);
@@ -40,6 +42,12 @@ struct Ctx {
                const int32_t* push, size_t n_push, uint64_t out_elems, const shp_epilogue* epi);
     int collect_timing();
 };
+
+// SHP_OK unless `stream` is being captured into a graph; then SHP_ERR_INVALID naming `what`.
+// Entry points that allocate, copy, clear memory or wait for the stream call it first, so a
+// call made between shp_capture_begin and shp_capture_end fails closed instead of recording
+// a memset or copy node into the caller's graph or breaking the capture.
+int refuse_while_capturing(hipStream_t stream, const char* what);
 
 // Resolves, once per device and with that device current, the device address of the fixed
 // split-K scratch array behind shp_launch_static (static_scratch.hip).

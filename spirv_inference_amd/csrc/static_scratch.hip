@@ -31,6 +31,11 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 float* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+// Per device: the stream of the last eager (uncaptured) static launch and an event recorded
+// after it, so a launch from another stream first waits for it instead of overwriting
+// partials and counters that launch may still be using.
+hipStream_t g_last_stream[kMaxDevices] = {};
+hipEvent_t g_last_done[kMaxDevices] = {};
 
 __global__ void zero_ints_kernel(int* p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -86,14 +91,44 @@ extern "C" int shp_launch_static(shp_ctx* ctx, const char* kernel, const void* i
                         std::to_string(need) + " bytes of split-K scratch, more than the " +
                         std::to_string(shp::kStaticScratchBytes) +
                         "-byte static scratch; use shp_launch_ex");
-    if (need > 0) {
-        // The array keeps the previous call's contents: start this launch's tile counters at
-        // zero with a fill kernel (capturable, unlike a memset node).
-        const int n = (int)(shp::kSplitCounterBytes / sizeof(int));
-        hipLaunchKernelGGL(shp::zero_ints_kernel, dim3((n + 255) / 256), dim3(256), 0, c->stream,
-                           reinterpret_cast<int*>(ws), n);
-        SHP_HIP_CHECK(hipGetLastError());
+    if (need == 0)  // no split-K scratch: nothing is shared
+        return shp::launch_kernel(c->stream, kernel, in0, in1, out, push, n_push, out_elems, epi,
+                                  ws, shp::kStaticScratchBytes, &c->tune);
+    // One array per GPU serves every context and stream.  Launches on one stream are ordered
+    // by it; a launch on another stream waits (on the device) for the last eager launch.  A
+    // stream under capture cannot wait for work outside its graph, so there the call is
+    // refused while that launch is still running.  Graph replays that overlap on one GPU
+    // still race: the caller orders them.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SHP_HIP_CHECK(hipStreamIsCapturing(c->stream, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(shp::g_mu);
+    hipEvent_t& done = shp::g_last_done[c->device];
+    hipStream_t& last = shp::g_last_stream[c->device];
+    if (last && last != c->stream) {
+        if (capturing) {
+            hipError_t q = hipEventQuery(done);
+            if (q == hipErrorNotReady)
+                return fail(SHP_ERR_UNSUPPORTED,
+                            "shp_launch_static: a launch on another stream may still use the "
+                            "static scratch; synchronise it before capturing");
+            if (q != hipSuccess)
+                return fail(SHP_ERR_HIP, std::string("shp_launch_static: ") + hipGetErrorString(q));
+        } else {
+            SHP_HIP_CHECK(hipStreamWaitEvent(c->stream, done, 0));
+        }
     }
-    return shp::launch_kernel(c->stream, kernel, in0, in1, out, push, n_push, out_elems, epi, ws,
-                              shp::kStaticScratchBytes, &c->tune);
+    // The array keeps the previous call's contents: start this launch's tile counters at
+    // zero with a fill kernel (capturable, unlike a memset node).
+    const int n = (int)(shp::kSplitCounterBytes / sizeof(int));
+    hipLaunchKernelGGL(shp::zero_ints_kernel, dim3((n + 255) / 256), dim3(256), 0, c->stream,
+                       reinterpret_cast<int*>(ws), n);
+    SHP_HIP_CHECK(hipGetLastError());
+    int rc = shp::launch_kernel(c->stream, kernel, in0, in1, out, push, n_push, out_elems, epi,
+                                ws, shp::kStaticScratchBytes, &c->tune);
+    if (rc || capturing) return rc;
+    if (!done) SHP_HIP_CHECK(hipEventCreateWithFlags(&done, hipEventDisableTiming));
+    SHP_HIP_CHECK(hipEventRecord(done, c->stream));
+    last = c->stream;
+    return SHP_OK;
 }

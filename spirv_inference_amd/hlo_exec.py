@@ -57,6 +57,7 @@ class HloOp:
     shape: list[int]
     attrs: dict[str, str]
     raw: str
+    result_type: str | None = None  # the type text before the opcode, e.g. f32[1,64]{1,0}
 
 
 def _attr(line: str, key: str) -> str | None:
@@ -102,7 +103,7 @@ def _parse_op(line: str) -> HloOp | None:
     shape = [int(d) for d in m.group(1).split(",") if d.strip().isdigit()] if m else []
     operands = [t.strip(",()") for t in rhs.split() if t.startswith("%")]
     attrs = {k: v for k in _ATTRS if (v := _attr(line, k)) is not None}
-    return HloOp(res[0], opcode, operands, shape, attrs, line)
+    return HloOp(res[0], opcode, operands, shape, attrs, line, rtype or None)
 
 
 def parse_hlo_text(text: str) -> list[HloOp]:
@@ -119,6 +120,21 @@ def parse_hlo_text(text: str) -> list[HloOp]:
         if in_entry and (op := _parse_op(t)) is not None:
             ops.append(op)
     return ops
+
+
+def module_name(text: str) -> str:
+    """The module's name as parser.rs:14-31 takes it: the token after `HloModule` (its
+    trailing comma dropped), or after `module @`; "module" when neither is present."""
+    name = "module"
+    for line in text.splitlines():
+        t = line.strip()
+        if t.startswith("HloModule "):
+            parts = t.split()
+            name = parts[1].rstrip(",") if len(parts) > 1 else "module"
+        if t.startswith("module @"):
+            parts = t.split()
+            name = parts[1].lstrip("@") if len(parts) > 1 else "@module"
+    return name
 
 
 def _ints(v: str | None) -> list[int]:
@@ -211,6 +227,28 @@ class DeviceBackend:
         g.destroy()
 
 
+class _Recorder:
+    """The backend with its launches noted by kernel name and element count, so every
+    launch can be attributed to the HLO op that issued it."""
+
+    def __init__(self, backend: Any):
+        self._b, self._log = backend, []
+
+    def __getattr__(self, name):
+        return getattr(self._b, name)
+
+    def launch(self, kernel, in0, in1, out, push, **kw):
+        n = kw.get("out_elems")
+        if n is None:
+            n = getattr(out, "n", None) or getattr(out, "size", None)
+        self._log.append((kernel, int(n) if n is not None else None))
+        return self._b.launch(kernel, in0, in1, out, push, **kw)
+
+    def take(self) -> list:
+        log, self._log = self._log, []
+        return log
+
+
 class HloExecutor:
     """Runs an ENTRY op list with compiler.rs's lowering on a backend."""
 
@@ -221,9 +259,21 @@ class HloExecutor:
             for name in op.operands:
                 self.last_use[name] = i
 
-    def run(self, params: Sequence[np.ndarray], keep: bool = False):
+    def run(self, params: Sequence[np.ndarray], keep: bool = False, on_value=None):
         """Execute with `params` in parameter order; returns the last op's value (a backend
-        tensor) and its shape.  keep=True keeps every intermediate in self.values."""
+        tensor) and its shape.  keep=True keeps every intermediate in self.values.
+
+        After each op, self.record holds (result, opcode, kernels launched for it) and
+        on_value(op, tensor, shape), when given, sees the op's value before any buffer is
+        released (the NaN trace of compiler.rs:613-623 hooks in here)."""
+        backend = self.b
+        self.b = _Recorder(backend)  # every launch, _dot's included, goes through it
+        try:
+            return self._run(params, keep, on_value)
+        finally:
+            self.b = backend
+
+    def _run(self, params, keep, on_value):
         b = self.b
         vals: dict[str, tuple[Any, list[int]]] = {}
         owner: dict[str, str] = {}   # value -> the name whose buffer it is (aliases share)
@@ -257,6 +307,7 @@ class HloExecutor:
                     b.launch("hlo_broadcast", one, None, out, H.broadcast_push((1,), shape, (0,)))
                     b.free(one)
             elif oc in ALIASES:
+                b.take()
                 src, _ = get(0)
                 vals[op.result] = (src, shape)
                 own = owner[op.operands[0]]
@@ -392,7 +443,9 @@ class HloExecutor:
             vals[op.result] = (out, shape)
             owner[op.result] = op.result
             end[op.result] = self.last_use.get(op.result, i)
-            self.record.append((op.result, oc))
+            self.record.append((op.result, oc, b.take()))
+            if on_value is not None:
+                on_value(op, out, shape)
             last = op.result
             self._release(i, vals, owner, end, keep)
         if last is None:

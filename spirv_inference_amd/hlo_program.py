@@ -52,9 +52,27 @@ _ACT_CANDIDATES = {
     4: lambda x: 1.0 / (1.0 + np.exp(-x)),
     5: np.tanh,
     6: lambda x: x / (1.0 + np.exp(-x)),
-    7: lambda x: 0.5 * x * np.array([math.erfc(-v / math.sqrt(2.0)) for v in x]),
+    7: lambda x: 0.5 * x * np.array([math.erfc(-v / math.sqrt(2.0)) if not math.isnan(v)
+                                      else math.nan for v in x]),
 }
-_PROBES = np.concatenate([np.linspace(-12.0, 12.0, 2401), [0.0, 1e-4, -1e-4, 0.5, -0.5]])
+# Probe values on which a region must equal an activation before it is fused: a dense sweep
+# of [-12, 12], then magnitudes out to the float32 limit (a clamp at 20 or 1e4 that equals
+# ReLU on the sweep differs there), the tiny and non-finite values.
+_WIDE = np.array([12.5, 15.0, 19.99, 20.0, 20.01, 25.0, 50.0, 88.0, 100.0, 1e3, 1e4, 1e5, 1e10,
+                  1e20, 1e30, 3.4e38, 1e-30, 1e-38])
+_PROBES = np.concatenate([np.linspace(-12.0, 12.0, 2401), [0.0, 1e-4, -1e-4, 0.5, -0.5],
+                          _WIDE, -_WIDE, [np.inf, -np.inf, np.nan]])
+
+
+def _same(y: np.ndarray, ref: np.ndarray) -> bool:
+    """y equals ref on every probe: within 1e-5 * (1 + |ref|) where ref is finite, the same
+    infinity where it is infinite, NaN where it is NaN."""
+    fin = np.isfinite(ref)
+    with np.errstate(invalid="ignore"):
+        close = np.abs(y[fin] - ref[fin]) <= 1e-5 * (1.0 + np.abs(ref[fin]))
+    inf = np.isinf(ref)
+    nan = np.isnan(ref)
+    return bool(np.all(close) and np.all(y[inf] == ref[inf]) and np.all(np.isnan(y[nan])))
 
 
 def _rm_strides(shape: Sequence[int]) -> tuple:
@@ -152,6 +170,8 @@ class HloProgram:
                 if o in self.consumers and i not in self.consumers[o]:
                     self.consumers[o].append(i)
         self.launches: list[tuple] = []
+        self.launch_src: list[str] = []  # the HLO result each launch is recorded for
+        self._cur = None
         self.pool: dict[int, list[Buf]] = {}
         self.owned: list[Buf] = []
         self.fused_counts: dict[str, int] = {}
@@ -348,8 +368,7 @@ class HloProgram:
                     env[op.result] = _eval_elementwise(op.opcode, args)
             y = np.broadcast_to(env[exit_name], _PROBES.shape)
             for code, f in _ACT_CANDIDATES.items():
-                ref = f(_PROBES)
-                if np.all(np.abs(y - ref) <= 1e-5 * (1.0 + np.abs(ref))):
+                if _same(y, f(_PROBES)):
                     return code
         return None
 
@@ -720,6 +739,7 @@ class HloProgram:
                 alpha=0.0, out_elems=None):
         self.launches.append((kernel, in0, in1, out, [int(p) for p in push], bias, residual,
                               int(act), float(alpha), out_elems))
+        self.launch_src.append(self._cur)
 
     def _new(self, shape: Sequence[int]) -> View:
         n = max(1, _n(shape))
@@ -761,6 +781,7 @@ class HloProgram:
             if i in self.absorbed and i not in self.groups:
                 self._release_after(i, eff)
                 continue
+            self._cur = op.result
             if i in self.groups:
                 v = self._lower_group(self.groups[i])
             elif op.opcode == "parameter":
@@ -775,6 +796,7 @@ class HloProgram:
             self._release_after(i, eff)
         outs = []
         for name in self._roots:
+            self._cur = name
             v = self.vals[name]
             temps: list = []
             c = self._contig(v, temps)
@@ -1054,25 +1076,52 @@ class HloProgram:
         else:
             push = [bo, bi, M, N, K, sa[0], sa[1], am, ak, sb[0], sb[1], bk, bn,
                     sc[0], sc[1], cm, cn]
-            if not (bias or residual or act) and self._fuse_attention(A, B, out, push):
+            if not (bias or residual or act) and self._fuse_attention(A, B, out, push, op):
                 return out
             self._launch("dot_general_strided", self._h(A), self._h(B), self._h(out), push,
                          out_elems=bsz * M * N, **e)
-            self._last_dot = (len(self.launches) - 1, A, B, out, push)
+            self._last_dot = (len(self.launches) - 1, A, B, out, push, op.result)
         return out
 
-    def _fuse_attention(self, P: View, V: View, out: View, push: list) -> bool:
+    def _readers(self, name: str) -> tuple[set, bool]:
+        """The ops that read `name`'s elements, looking through the view ops that alias it
+        (reshape / convert / transpose), and whether `name` or one of those views is a
+        program output."""
+        out, root, todo, seen = set(), False, [name], set()
+        while todo:
+            cur = todo.pop()
+            if cur in seen:
+                continue
+            seen.add(cur)
+            root = root or cur in self._roots
+            for c in self.consumers.get(cur, []):
+                if self.ops[c].opcode in ("reshape", "convert", "transpose"):
+                    todo.append(self.ops[c].result)
+                else:
+                    out.add(c)
+        return out, root
+
+    def _fuse_attention(self, P: View, V: View, out: View, push: list, ctx_op: HloOp) -> bool:
         """The context dot of an attention block: when the two launches before it are the
         scores dot (Q . K^T) and the row softmax that reads it, and this dot reads the softmax's
         output, with Q, K and V column blocks of one row-major buffer (sequence 128, head dim
         64, heads side by side, the layout of a fused QKV activation), replace the three by
-        one `attention_fused` launch (the C++ graph's op for the same block)."""
+        one `attention_fused` launch (the C++ graph's op for the same block).  The fused
+        launch writes neither the scores nor the probabilities, so it is taken only when
+        nothing else reads them: the probabilities only by this dot, the scores only by the
+        softmax, and neither is a program output."""
         sm, dt = getattr(self, "_last_softmax", None), getattr(self, "_last_dot", None)
         n = len(self.launches)
         if sm is None or dt is None or sm[0] != n - 1 or dt[0] != n - 2:
             return False
-        _, x, y, mask, bits = sm
-        _, Q, K, S_out, sp = dt
+        _, x, y, mask, bits, g = sm
+        _, Q, K, S_out, sp, scores_name = dt
+        probs, root = self._readers(self.ops[g["anchor"]].result)
+        if root or probs != {self.idx[ctx_op.result]}:
+            return False
+        scores, root = self._readers(scores_name)
+        if root or not scores <= set(g["members"]) | {g["anchor"]}:
+            return False
         B, H, S, _, HD = sp[:5]
         if S != 128 or HD != 64 or push[:5] != [B, H, S, HD, S]:
             return False
@@ -1100,6 +1149,7 @@ class HloProgram:
             return False
         total = B * S * ld_out
         self.launches = self.launches[:-2]
+        self.launch_src = self.launch_src[:-2]
         self._last_softmax = self._last_dot = None
         self.fused_counts["softmax"] -= 1
         if not self.fused_counts["softmax"]:
@@ -1165,7 +1215,7 @@ class HloProgram:
                 bits = int(np.array([g["scale"]], np.float32).view(np.int32)[0])
                 self._launch("softmax_rows", self._h(x), self._h(mask) if mask else None,
                              self._h(out), [g["rows"], g["cols"], bits], out_elems=out.n)
-                self._last_softmax = (len(self.launches) - 1, x, out, mask, bits)
+                self._last_softmax = (len(self.launches) - 1, x, out, mask, bits, g)
                 self._note("softmax")
                 return out
             if kind in ("layernorm", "rmsnorm"):
@@ -1232,11 +1282,53 @@ class HloProgram:
             self._warm = True
         return self.outputs()
 
-    def _replay(self) -> None:
+    def _replay(self, after=None) -> None:
         launch = self.b.launch
-        for (k, a, b, c, push, bias, res, act, alpha, oe) in self.launches:
+        for i, (k, a, b, c, push, bias, res, act, alpha, oe) in enumerate(self.launches):
             launch(k, a, b, c, push, bias=bias, residual=res, act=act, alpha=alpha,
                    out_elems=oe)
+            if after is not None:
+                after(i)
+
+    def run_traced(self, after) -> list:
+        """One eager replay calling after(i) once launch i is enqueued (its output handle is
+        self.launches[i][3]): per-launch checks such as the NaN trace, before a later launch
+        reuses the buffer."""
+        self._replay(after)
+        self._warm = True
+        return self.outputs()
+
+    def steps(self) -> list[dict]:
+        """The ENTRY ops in order with what became of each: the `steps` list of the HLO
+        runner's report (compiler.rs:226-232 GraphStep).  `execution` names the lowering
+        (a launch, a fused group, a strided view or an alias) and `spv_name` the first
+        registry kernel launched for the op (None when it launches nothing)."""
+        kernels: dict[str, list] = {}
+        for (k, *_rest), src in zip(self.launches, self.launch_src):
+            kernels.setdefault(src, []).append(k)
+        anchor_of = {m: a for a, g in self.groups.items() for m in g["members"]}
+        out = []
+        for i, op in enumerate(self.ops):
+            ks = kernels.get(op.result, [])
+            if i in anchor_of and i not in self.groups:
+                ex = f"fused_into {self.ops[anchor_of[i]].result}"
+            elif i in self.groups:
+                ex = f"hip_fused_{self.groups[i]['kind']}"
+            elif op.opcode == "parameter":
+                ex = "bound_parameter"
+            elif op.opcode == "constant":
+                ex = "materialized scalar constant"
+            elif op.opcode in ("tuple", "get-tuple-element"):
+                ex = "tuple_alias"
+            elif ks:
+                ex = "hip_" + "+".join(dict.fromkeys(ks))
+            elif op.opcode in ("reshape", "convert"):
+                ex = "metadata_reshape"
+            else:
+                ex = "strided_view"
+            out.append({"result": op.result, "opcode": op.opcode, "execution": ex,
+                        "elements": _n(op.shape), "spv_name": ks[0] if ks else None})
+        return out
 
     def outputs(self) -> list:
         """(handle, shape) of each ROOT value, contiguous."""
@@ -1254,6 +1346,7 @@ class HloProgram:
             self.b.free(buf.handle)
         self.owned = []
         self.launches = []
+        self.launch_src = []
 
 
 def _batch2(v: View, dims: Sequence[int]):

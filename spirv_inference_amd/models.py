@@ -159,6 +159,12 @@ class Llama:
         check(lib().shp_llama_engine(self.handle, C.byref(e)), "shp_llama_engine")
         return {v: k for k, v in self.ENGINES.items()}[e.value]
 
+    def set_wait_limit(self, polls: int = -1):
+        """Bound of the persistent engine's grid waits in polls (-1: the default).  A wait
+        that gives up ends the decode call with ShpError (SHP_ERR_HIP) and leaves the state
+        undefined until reset()."""
+        check(lib().shp_llama_set_wait_limit(self.handle, int(polls)), "shp_llama_set_wait_limit")
+
     def step(self, token: int):
         check(lib().shp_llama_step(self.handle, int(token)), "shp_llama_step")
 

@@ -193,6 +193,19 @@ class Context:
             i += 1
         return out
 
+    def timing_launches(self) -> list[tuple[str, float]]:
+        """Every timed launch since the last reset, in issue order: (kernel, elapsed ms)."""
+        n = C.c_uint64()
+        check(lib().shp_timing_launch_count(self.handle, C.byref(n)), "shp_timing_launch_count")
+        name = C.create_string_buffer(128)
+        ms = C.c_double()
+        out = []
+        for i in range(n.value):
+            check(lib().shp_timing_launch(self.handle, i, name, 128, C.byref(ms)),
+                  "shp_timing_launch")
+            out.append((name.value.decode(), ms.value))
+        return out
+
 
 class Graph:
     """A recorded launch sequence (shp_graph): launch() replays it on the context stream."""

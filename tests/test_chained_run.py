@@ -47,3 +47,21 @@ def test_oracle_chain_matches_float64():
         np.testing.assert_allclose(o[k], n[k], rtol=1e-5, atol=1e-6, err_msg=k)
     assert (o["relu_output"] == 0).any() and (o["relu_output"] > 0).any()
     assert abs(float(o["softmax_output"].sum()) - 1.0) < 1e-5
+
+
+def test_cli_fails_on_an_unreadable_spv_path(tmp_path, capsys):
+    """main.rs:109-120: a --*-spv path that cannot be read ends the run with an error naming
+    it, before any device work and without a report."""
+    from chained_fixture import write_manifest
+    manifest = write_manifest(tmp_path)
+    ok = tmp_path / "ok.spv"
+    ok.write_bytes(b"\x03\x02\x23\x07")
+    missing = tmp_path / "typo" / "relu.spv"
+    argv = ["--device", "any", "--conv2d-spv", str(ok), "--batchnorm-spv", str(ok),
+            "--relu-spv", str(missing), "--softmax-spv", str(ok),
+            "--fixture-manifest", str(manifest), "--report", str(tmp_path / "r.json"),
+            "--dump-dir", str(tmp_path / "dump")]
+    assert CR.main(argv) == 1
+    assert str(missing) in capsys.readouterr().err
+    assert not (tmp_path / "r.json").exists()
+    assert CR.spv_entry(str(ok))["sha256"] == __import__("hashlib").sha256(ok.read_bytes()).hexdigest()

@@ -13,9 +13,15 @@ pytestmark = pytest.mark.gpu
 
 
 def _cli(tmp_path, manifest, graph=False):
-    argv = ["--device", "any", "--conv2d-spv", str(tmp_path / "none.spv"),
-            "--batchnorm-spv", str(tmp_path / "none.spv"), "--relu-spv", str(tmp_path / "none.spv"),
-            "--softmax-spv", str(tmp_path / "none.spv"), "--fixture-manifest", str(manifest),
+    # main.rs:109-120 reads the four shader files before running; their bytes are only
+    # recorded here, so any readable file stands in for them
+    spv = {}
+    for k in ("conv2d", "batchnorm", "relu", "softmax"):
+        spv[k] = tmp_path / f"{k}.spv"
+        spv[k].write_bytes(k.encode())
+    argv = ["--device", "any", "--conv2d-spv", str(spv["conv2d"]),
+            "--batchnorm-spv", str(spv["batchnorm"]), "--relu-spv", str(spv["relu"]),
+            "--softmax-spv", str(spv["softmax"]), "--fixture-manifest", str(manifest),
             "--report", str(tmp_path / "report.json"), "--dump-dir", str(tmp_path / "dump")]
     rc = CR.main(argv + (["--graph"] if graph else []))
     return rc, json.loads((tmp_path / "report.json").read_text())

@@ -99,7 +99,7 @@ ENTRY %main (a: f32[4,6,3], b: f32[3,4,5]) -> f32[4,6,5] {
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
 
 
-def test_cli_validate_only_and_unsupported(tmp_path, capsys):
+def test_cli_validate_only_and_unsupported(tmp_path, capsys, monkeypatch):
     from spirv_inference_amd import hlo_run
     p = tmp_path / "m.txt"
     p.write_text(fixture_text("bert_base"))
@@ -109,9 +109,12 @@ def test_cli_validate_only_and_unsupported(tmp_path, capsys):
     capsys.readouterr()
     q = tmp_path / "g.txt"
     q.write_text(SYNTH.replace("exponential(", "gather("))
+    # without --report the report still goes to main.rs:8's default path
+    monkeypatch.chdir(tmp_path)
     assert hlo_run.main(["--input", str(q), "--validate-only"]) == 0
     rep = json.loads(capsys.readouterr().out)
     assert rep["status"] == "blocked_unsupported_feature" and "gather" in rep["validation"]["reason"]
+    assert json.loads((tmp_path / "xla_hlo/reports/hlo_report.json").read_text()) == rep
 
 
 def test_cli_compare_follows_tensor_rs():

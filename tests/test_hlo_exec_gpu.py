@@ -95,5 +95,15 @@ def test_cli_runs_fixture_with_reference_flags(tmp_path):
     import json
     rep = json.loads((tmp_path / "r.json").read_text())
     assert rc == 0 and rep["status"] == "pass", rep["execution"]
-    assert rep["execution"]["device"]["vendor_id"] == 0x1002
-    assert (tmp_path / "out.raw.f32").stat().st_size == 4 * rep["execution"]["output"]["elements"]
+    ex = rep["execution"]
+    assert ex["device"]["vendor_id"] == 0x1002 and ex["device"]["probe_output"] == [3.0]
+    assert (tmp_path / "out.raw.f32").stat().st_size == 4 * ex["output"]["elements"]
+    # compiler.rs:652-667: one record per device launch, each with its own hipEvent time
+    assert ex["dispatch_count"] == len(ex["dispatches"]) > 0
+    assert all(d["elapsed_ms"] > 0 and d["device_name"] == ex["device"]["name"]
+               for d in ex["dispatches"])
+    assert len(ex["steps"]) == len(ops) and ex["final_result"] == ops[-1].result
+    assert ex["parity"]["epsilon"] == np.float32(1e-3)
+    assert rep["module"]["ops"][0]["result"] == ops[0].result
+    print(f"[hlo_run] {ex['dispatch_count']} dispatches, "
+          f"{sum(d['elapsed_ms'] for d in ex['dispatches']):.3f} ms of kernel time", flush=True)

@@ -194,6 +194,12 @@ def _act_module(body):
     (lambda b, v: b.gelu_erf(v), 7),
     (lambda b, v: b.binary("multiply", v, v), 0),                       # x^2: not an epilogue
     (lambda b, v: b.binary("maximum", v, b.splat(0.5, v.shape)), 0),     # max(x, 0.5)
+    # ReLU only on [-12, 12]: clamps at 20 and 1e4 are not ReLU and must not fuse as it
+    (lambda b, v: b.binary("minimum", b.relu(v), b.splat(20.0, v.shape)), 0),
+    (lambda b, v: b.binary("minimum", b.relu(v), b.splat(1e4, v.shape)), 0),
+    # tanh.comp's clamp to +-20 before tanh is tanh everywhere in float (tanh(20) rounds to 1)
+    (lambda b, v: b.unary("tanh", b.binary("maximum", b.binary("minimum", v, b.splat(20.0, v.shape)),
+                                          b.splat(-20.0, v.shape))), 5),
 ])
 def test_activation_regions(body, act):
     text = _act_module(body)
@@ -220,3 +226,31 @@ def test_reshape_views_follow_numpy():
             continue
         got = np.lib.stride_tricks.as_strided(base, r.shape, [s * 4 for s in r.strides])
         np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("extra", ["probs", "scores"])
+def test_attention_not_fused_when_probs_or_scores_are_read_elsewhere(extra):
+    """The fused attention launch writes neither the scores nor the probabilities: when a
+    program output also reads either of them, the three launches stay, and every output
+    (the probabilities' rows summing to 1) matches float64 numpy."""
+    text, _ = G.bert_base(1, 128, 1, 128, 2, 256)
+    ops = X.parse_hlo_text(text)
+    root = next(o for o in ops if o.raw.lstrip().startswith("ROOT"))
+    if extra == "probs":  # the softmax's divide
+        other = next(o for o in ops if o.opcode == "divide")
+    else:  # the scores dot, the first dot with batch dims
+        other = next(o for o in ops if o.opcode == "dot" and "lhs_batch_dims" in o.raw)
+    ty = lambda o: o.raw.split("=", 1)[1].split()[0]
+    line = root.raw.strip()
+    text2 = text.replace(line, line.replace("ROOT ", "", 1) + "\n  ROOT %out = (" + ty(root) +
+                         ", " + ty(other) + ") tuple(" + ty(root) + " " + root.result + ", " +
+                         ty(other) + " " + other.result + ")")
+    ops2 = X.parse_hlo_text(text2)
+    params = seeded_params(ops2, seed=7)
+    _, prog, outs = _run(text2, params)
+    assert "attention" not in prog.fused_counts and prog.fused_counts.get("softmax") == 1
+    allv = eval_numpy(ops2, params, all_values=True)
+    assert_close(outs[0], allv[root.result], 1e-4, 1e-4, "hidden output")
+    assert_close(outs[1], allv[other.result], 1e-4, 1e-4, f"{extra} output")
+    if extra == "probs":
+        assert np.allclose(outs[1].sum(-1), 1.0, atol=1e-5)

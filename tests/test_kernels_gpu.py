@@ -857,3 +857,18 @@ def test_hlo_shape_ops_fail_closed(ctx):
         _dev(ctx, "hlo_transpose", rnd(4), None, 4, [2, 4, 2, 2, 0, 0])
     with pytest.raises(RuntimeError):  # total does not match the output
         _dev(ctx, "hlo_slice", rnd(4, 6), None, 5, H.slice_push((4, 6), (0, 0), (2, 6)))
+
+
+@pytest.mark.parametrize("n,nan_at", [(0, []), (7, []), (7, [3]), (4099, [4098, 17, 2000]),
+                                      (1 << 22, [(1 << 22) - 1, 123457, 1 << 21])])
+def test_nan_count(ctx, orc, n, nan_at):
+    """The HLO runner's NaN trace kernel: count and first index, bit-exact (inf is not NaN)."""
+    x = rnd(max(n, 1))[:n].copy() if n else np.zeros(1, np.float32)
+    if n:
+        x[::97] = np.inf
+    for i in nan_at:
+        x[i] = np.nan
+    y, r = both(ctx, orc, "nan_count", x, None, 2, [n])
+    assert y.tobytes() == r.tobytes()
+    c = y.view(np.int32)
+    assert c[0] == len(nan_at) and c[1] == (min(nan_at) if nan_at else -1)

@@ -86,6 +86,26 @@ def test_cnn_per_op_and_top1(ctx, orc, arch, batch):
         assert_rankings_match(logits_gpu, host[out_logits], batch, arch)
 
 
+def test_resnet50_b32_headline_per_op(ctx, orc):
+    """The headline config exactly as bench.py builds it (ResNet-50 v1.5, batch 32, seed 2):
+    every one of its ops (the 53 convolutions with their b32 plans: 64x64/k16 tiles with 2-3
+    splits, k32 with 5 splits and a reduction pass, the persistent K=64 kernel, the 7x7 stem;
+    then pools, FC and softmax) against the oracle on the GPU's own inputs at 1e-4/1e-4.
+    Logs each op and the worst layer relative to its gate."""
+    from oracle import walk
+    from spirv_inference_amd.models import Model
+    with Model(ctx, "resnet50_v1_5", 32, seed=2) as m:
+        m.run()
+        ctx.sync()
+        recs = check_per_op(m, walk)
+        convs = [r for r in recs if r["kernel"] == "hlo_conv_nhwc_hwio"]
+        assert len(convs) == 53, len(convs)
+        worst = max(recs, key=lambda r: r["worst_excess"])
+        print(f"[resnet50 b32] {len(recs)} ops within 1e-4/1e-4; worst op {worst['index']} "
+              f"{worst['label']} max_abs={worst['max_abs']:.2e} "
+              f"excess={worst['worst_excess']:.2e}", flush=True)
+
+
 def test_bert_base_per_op(ctx, orc):
     from oracle import walk
     from spirv_inference_amd.models import Model
@@ -420,3 +440,71 @@ def test_captured_graph_survives_workspace_growth():
                     big.run()
             c.sync()
             junk.free()
+
+
+def test_persistent_wait_gives_up_then_reset_recovers(ctx, orc):
+    """The persistent engine's bounded waits, forced to give up from the host (a limit of 0
+    polls, checked at the first missed poll): every workgroup exits, the call reports
+    SHP_ERR_HIP (run_llama_spirv.py:76-81,237-246 abort on a non-zero status), and after
+    reset() a fresh decode gives the oracle's tokens."""
+    from spirv_inference_amd import ShpError
+    from spirv_inference_amd._lib import SHP_ERR_HIP
+    from spirv_inference_amd.models import Llama
+    rng = np.random.default_rng(9)
+    prompt = [int(t) for t in rng.integers(0, SMALL["vocab"], 8)]
+    with Llama(ctx, seed=10, **SMALL) as lm:
+        lm.set_engine("persistent")
+        lm.reset()
+        for t in prompt[:3]:
+            lm.step(t)
+        print("[llama abort] decode with wait limit 0", flush=True)
+        lm.set_wait_limit(0)
+        with pytest.raises(ShpError, match="timed out") as ei:
+            lm.decode(4)
+        assert ei.value.code == SHP_ERR_HIP
+        print("[llama abort] gave up as forced; reset and decode again", flush=True)
+        lm.set_wait_limit(-1)
+        lm.reset()
+        for t in prompt:
+            lm.step(t)
+        lm.decode(5)
+        want, logits, _ = oracle_decode(orc, lm, SMALL, prompt, 6)
+        assert lm.tokens()[len(prompt) - 1:] == want
+        assert_close(lm.logits(), logits[-1], 1e-4, 1e-4, "logits after recovery")
+
+
+def test_calls_that_allocate_or_wait_are_refused_under_capture(ctx):
+    """Between capture_begin and capture_end, every entry point that would allocate, copy,
+    clear memory or wait for the stream returns SHP_ERR_INVALID instead of recording into
+    the caller's graph; the capture stays usable and the calls work again after it."""
+    from spirv_inference_amd import KernelRun, ShpError
+    from spirv_inference_amd._lib import SHP_ERR_INVALID
+    from spirv_inference_amd.models import Llama, Model
+    with Llama(ctx, seed=5, **SMALL) as lm, Model(ctx, "mobilenet_v2", 1, seed=2) as m:
+        t = ctx.tensor(np.arange(8, dtype=np.float32))
+        y = ctx.empty(8)
+        m.use_graph(True)
+        ctx.sync()
+        ctx.capture_begin()
+        refused = {
+            "llama_reset": lm.reset, "llama_step": lambda: lm.step(1),
+            "llama_decode": lambda: lm.decode(1), "llama_tokens": lm.tokens,
+            "run_kernel": lambda: ctx.run_kernel(KernelRun("p", "relu", np.ones(4, np.float32),
+                                                           np.ones(1, np.float32), 4, 1, [4])),
+            "download": t.download, "upload": lambda: t.upload(np.zeros(8, np.float32)),
+            "sync": ctx.sync, "timing_reset": ctx.timing_reset, "model_run_graph": m.run,
+        }
+        for name, call in refused.items():
+            with pytest.raises(ShpError) as ei:
+                call()
+            assert ei.value.code == SHP_ERR_INVALID and "captured" in str(ei.value), name
+        ctx.launch("relu", t, None, y, [8])  # launches are still recorded
+        g = ctx.capture_end()
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(y.download(), np.arange(8, dtype=np.float32))
+        g.destroy()
+        lm.reset()
+        ctx.sync()
+        for x in (t, y):
+            x.free()

@@ -83,3 +83,35 @@ def test_static_scratch_rejects_plans_beyond_its_size():
         ctx.sync()
         for t in (a, b, c):
             t.free()
+
+
+def test_static_scratch_orders_launches_from_two_streams():
+    """Two contexts (two streams) issue static launches back to back with no host wait in
+    between: the second waits on the device for the first (the array is shared per GPU), so
+    both equal their workspace-launched results bit for bit."""
+    with Context("any") as ca, Context("any") as cb, Context("any") as cw:
+        print("[no_alloc] two streams on the static scratch: conv4 on A, conv5 on B", flush=True)
+        want = [_conv(cw, lib().shp_launch_ex, s, seed=21 + i) for i, s in enumerate((CONV4, CONV5))]
+        bufs = []
+        for i, (c, shape) in enumerate(((ca, CONV4), (cb, CONV5))):
+            push = _push(**shape)
+            n, ih, ic, oc = shape["n"], shape["ih"], shape["ic"], shape["oc"]
+            x = c.fill_random(c.empty(n * ih * ih * ic), 21 + i, 1)
+            w = c.fill_random(c.empty(9 * ic * oc), 21 + i, 2, "normal", 0.0,
+                              float(np.sqrt(2 / (9 * ic))))
+            b = c.fill_random(c.empty(oc), 21 + i, 3, "normal", 0.0, 0.01)
+            r = c.fill_random(c.empty(push[13]), 21 + i, 4)
+            y = c.empty(push[13])
+            bufs.append((c, x, w, b, r, y, push))
+        for c, x, w, b, r, y, push in bufs:  # inputs ready before either launch
+            c.sync()
+        for c, x, w, b, r, y, push in bufs:
+            arr = (C.c_int32 * len(push))(*push)
+            epi = Epilogue(b.ptr, r.ptr, 1, 0.0)
+            check(lib().shp_launch_static(c.handle, b"hlo_conv_nhwc_hwio", x.ptr, w.ptr, y.ptr,
+                                          arr, len(push), push[13], C.byref(epi)), "static")
+        for (c, x, w, b, r, y, push), ref in zip(bufs, want):
+            c.sync()
+            assert np.array_equal(y.download(), ref)
+            for t in (x, w, b, r, y):
+                t.free()
