@@ -246,12 +246,48 @@ def bench_config(ctx, arch: str, batch: int, seq_len: int, steps: int):
         m.run()
     ctx.sync()
     ms = (time.perf_counter() - t0) / steps * 1e3
+    tfl = time_tflite_executor(ctx, m, steps) if arch in ("mobilenet_v2", "efficientnet_lite0") \
+        else None
     m.close()
     tflops = flops / (ms / 1e3) / 1e12
     return {"batch": batch, "seq_len": seq_len or None, "ms_per_forward": round(ms, 4),
             "gflop_per_forward": round(flops / 1e9, 3), "weight_mb": round(wbytes / 1e6, 2),
             "achieved_tflops": round(tflops, 3),
-            "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4)}
+            "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "tflite_executor": tfl}
+
+
+def time_tflite_executor(ctx, m, steps: int):
+    """The same forward through the TFLite front end: the resident graph exported to a TFL3
+    file, parsed, and run by TfliteExecutor on the graph's input, eagerly (one ctypes launch
+    per op from Python) and replayed from the executor's hipGraph (host clock, K
+    forwards each).  Its output must equal the graph's bit for bit."""
+    from spirv_inference_amd import tflite as T
+    m.run()
+    ctx.sync()
+    want = m.output(0).download()
+    model = T.parse_model(T.model_to_tflite(m))
+    ex = T.TfliteExecutor(ctx, model)
+    try:
+        ex.set_input(m.input(0).download())
+        out = {}
+        for mode in ("eager", "graph"):
+            for _ in range(3):
+                ex.run(graph=mode == "graph")
+            ctx.sync()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                ex.run(graph=mode == "graph")
+            ctx.sync()
+            out[f"{mode}_ms_per_forward"] = round((time.perf_counter() - t0) / steps * 1e3, 4)
+        out["identical_to_graph"] = bool(ex.output().tobytes() == want.tobytes())
+        out["operators"] = len(model.operators)
+        out["launches"] = sum(len(o["dispatches"]) for o in ex.op_log)
+        out["region"] = ("the graph exported to TFL3 -> parse_model -> TfliteExecutor; eager: "
+                         "one launch per op from Python; graph: one hipGraph replay per forward")
+        return out
+    finally:
+        ex.close()
 
 
 def bench_elementwise(ctx, elems: int = 64 << 20, reps: int = 20):
@@ -435,6 +471,11 @@ def main() -> int:
             c = configs[arch]
             log(f"{arch} b{b}: {c['ms_per_forward']:.3f} ms/forward, "
                 f"{c['achieved_tflops']:.1f} TFLOP/s ({100 * c['frac_fp32_mfma']:.1f}% of fp32 MFMA)")
+            if c["tflite_executor"]:
+                t = c["tflite_executor"]
+                log(f"{arch} b{b} via the TFLite executor: {t['graph_ms_per_forward']:.3f} ms "
+                    f"(hipGraph), {t['eager_ms_per_forward']:.3f} ms (eager); output identical "
+                    f"to the graph: {t['identical_to_graph']}")
     dec = None
     if not args.no_decode:
         dec = bench_decode(ctx, args.decode_tokens, args.prompt_tokens)

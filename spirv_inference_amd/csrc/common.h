@@ -33,9 +33,10 @@ int fail(int code, const std::string& msg);
 // bl: the buffer-loaded GEMM kernel never (-1) or, where its operand forms allow it, always
 // (1); with bl 1, tile 1/2/3 and bk 16/32/64 pick its tile; sk -1: never the persistent
 // small-K kernel (K 64 row products), else wherever it applies; stem -1: never the 7x7
-// 3-channel convolution kernel, else wherever it applies.
+// 3-channel convolution kernel, else wherever it applies; group: see below.
 struct GemmTune {
     int tile = 0, bk = 0, splits = 0, dma = 0, pg = 0, table = 0, dw = 0, bl = 0, sk = 0, stem = 0;
+    int group = 0;  // tile-row band of the tile order: 0 automatic, -1 row major, k > 0 forced
 };
 
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.

@@ -48,6 +48,9 @@ struct GemmParams {
     float* partial;   // [splits][batch][M][N] workspace when splits > 1
     int* counters;    // per-tile arrival counters (zero between launches) when fixup
     int fixup;        // 1: the last split of a tile sums the partials and applies the epilogue
+    // tile order: bands of group_m tile rows, each band walked column by column (1: row
+    // major); each XCD then takes a contiguous run of that order (tile_coords)
+    int group_m;
 };
 
 // The first kSplitCounterBytes of a split-K workspace hold the per-tile arrival counters of

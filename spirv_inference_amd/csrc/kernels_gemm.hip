@@ -25,6 +25,38 @@ namespace {
 using shp::GemmParams;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Output tile (tm, tn) and K split of this workgroup.  The grid is (tiles, splits, batch);
+// a workgroup's linear id within its batch slice, y * tiles + x, runs on XCD id % 8, and each
+// XCD has its own L2.  The first (total / 8) * 8 ids are renumbered so XCD x takes the
+// contiguous run [x * total / 8, (x + 1) * total / 8) of an order in which the split varies
+// slowest (the rest keep their ids): with 2, 4 or 8 splits each XCD then works inside one K
+// range and reads only that range of A and B.  Within a split the order walks bands of
+// `group` tile rows column by column, so a run covers about group rows x (run / group)
+// columns: A and B panels read by one XCD ~ group + run / group instead of 1 + run (row
+// major, group 1) when a run spans many columns.  `tile` = tm * tiles_n + tn identifies the
+// tile across its splits (the split-K arrival counters).
+struct WgCoords {
+    int tm, tn, split, tile;
+};
+__device__ __forceinline__ WgCoords wg_coords(int tiles_m, int tiles_n, int splits, int group) {
+    const int ntiles = tiles_m * tiles_n;
+    const int total = ntiles * splits;
+    int pos = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    const int full = (total / 8) * 8;
+    if (pos < full) pos = (pos % 8) * (full / 8) + pos / 8;
+    WgCoords c;
+    c.split = pos / ntiles;
+    const int t = pos - c.split * ntiles;
+    const int g = group > 1 ? group : 1;
+    const int band = t / (g * tiles_n);
+    const int within = t - band * g * tiles_n;
+    const int rows = min(g, tiles_m - band * g);
+    c.tm = band * g + within % rows;
+    c.tn = within / rows;
+    c.tile = c.tm * tiles_n + c.tn;
+    return c;
+}
+
 // Device-coherent (agent scope) 16-byte store and load of global memory, as two 8-byte
 // relaxed atomics: data written this way by one workgroup is read correctly by a workgroup
 // on another XCD (whose L2 is not coherent with the writer's) within the same launch.
@@ -281,14 +313,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     // the workgroups sharing A rows / B columns meet in the same L2.
     const int tiles_n = (p.N + BN - 1) / BN;
     const int tiles_m = (p.M + BM - 1) / BM;
-    const int ntiles = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    const int full = (ntiles / 8) * 8;
-    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
-    const int tm = bid / tiles_n, tn = bid % tiles_n;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const WgCoords wc = wg_coords(tiles_m, tiles_n, p.splits, p.group_m);
+    const int m0 = wc.tm * BM, n0 = wc.tn * BN;
 
-    const int split = blockIdx.y;
+    const int split = wc.split;
     const int bz = blockIdx.z;
     const int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
     const float* __restrict__ A = p.a + bo * p.sa_outer + bi * p.sa_inner;
@@ -585,7 +613,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     }
 
     gemm_epilogue<BM, BN, WM, WN, RC, CS, CM>(p, acc, smem, m0, n0, split, p.splits, bz, bo, bi,
-                                              gridDim.z, (int64_t)bz * gridDim.x + blockIdx.x);
+                                              gridDim.z, (int64_t)bz * gridDim.x + wc.tile);
 }
 
 // ---- buffer-loaded variant (gemm_bl_kernel) for the row-contiguous operand forms of the
@@ -658,13 +686,10 @@ __global__ __launch_bounds__(256) void gemm_bl_kernel(GemmParams p) {
 
     const int tiles_n = (p.N + BN - 1) / BN;
     const int tiles_m = (p.M + BM - 1) / BM;
-    const int ntiles = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    const int full = (ntiles / 8) * 8;
-    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
-    const int m0 = (bid / tiles_n) * BM, n0 = (bid % tiles_n) * BN;
+    const WgCoords wc = wg_coords(tiles_m, tiles_n, p.splits, p.group_m);
+    const int m0 = wc.tm * BM, n0 = wc.tn * BN;
 
-    const int split = blockIdx.y;
+    const int split = wc.split;
     const int bz = blockIdx.z;
     const int bo = bz / p.batch_inner, bi = bz % p.batch_inner;
     const float* A = p.a + bo * p.sa_outer + bi * p.sa_inner;
@@ -836,7 +861,7 @@ __global__ __launch_bounds__(256) void gemm_bl_kernel(GemmParams p) {
 
     gemm_epilogue<BM, BN, 2, 2, RC, CS, shp::C_STRIDED>(p, acc, smem, m0, n0, split, p.splits, bz,
                                                         bo, bi, gridDim.z,
-                                                        (int64_t)bz * gridDim.x + blockIdx.x);
+                                                        (int64_t)bz * gridDim.x + wc.tile);
 }
 
 // ---- persistent small-K variant (gemm_smallk_kernel) for products with K = 64 (KT) whose
@@ -1407,15 +1432,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, BN == 12
     __shared__ __attribute__((aligned(1024))) char smem[T::SMEM];
     const int tiles_n = (p.N + BN - 1) / BN;
     const int tiles_m = (p.M + T::BM - 1) / T::BM;
-    const int ntiles = tiles_m * tiles_n;
-    int bid = blockIdx.x;
-    const int full = (ntiles / 8) * 8;
-    if (bid < full) bid = (bid % 8) * (full / 8) + bid / 8;
-    const int kbeg = blockIdx.y * p.k_per_split;
+    const WgCoords wc = wg_coords(tiles_m, tiles_n, p.splits, p.group_m);
+    const int kbeg = wc.split * p.k_per_split;
     const int kend = min(p.K, kbeg + p.k_per_split);
-    dma_segment<BN, AM>(p, smem, (bid / tiles_n) * T::BM, (bid % tiles_n) * BN, blockIdx.z, kbeg,
-                        kend, blockIdx.y, p.splits, gridDim.z,
-                        (int64_t)blockIdx.z * gridDim.x + blockIdx.x);
+    dma_segment<BN, AM>(p, smem, wc.tm * T::BM, wc.tn * BN, blockIdx.z, kbeg,
+                        kend, wc.split, p.splits, gridDim.z,
+                        (int64_t)blockIdx.z * gridDim.x + wc.tile);
 }
 
 // Split-K second pass: sum the partials in split order, then the epilogue.
@@ -2031,6 +2053,59 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
                     gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED, tune));
 }
 
+// Band height of the tile order (GemmParams::group_m, see wg_coords).  For each candidate
+// height g it counts, per XCD, the distinct tile rows (A panels, BM x K-range each) and tile
+// columns (B panels, K-range x BN) its run of the split-major order touches, and keeps the g
+// with the fewest panel bytes summed over the 8 XCDs (row major, g = 1, on ties).  Tile
+// results do not depend on the order, only which L2 serves the panels.
+int64_t xcd_panel_cost(int tiles_m, int tiles_n, int splits, int g, int bm, int bn) {
+    const int64_t ntiles = (int64_t)tiles_m * tiles_n, total = ntiles * splits;
+    const int64_t run = total / 8;
+    if (run == 0) return 0;
+    int64_t cost = 0;
+    for (int x = 0; x < 8; ++x) {
+        int64_t a = x * run;
+        const int64_t end = a + run;
+        while (a < end) {  // one split's part of the run: [a, b)
+            const int64_t split_end = (a / ntiles + 1) * ntiles;
+            const int64_t b = std::min(end, split_end);
+            const int64_t t0 = a % ntiles, t1 = t0 + (b - a);  // [t0, t1) within the split
+            int64_t rows = 0, col_lo = tiles_n, col_hi = -1;
+            for (int64_t t = t0; t < t1;) {  // band by band
+                const int64_t band = t / ((int64_t)g * tiles_n);
+                const int64_t h = std::min<int64_t>(g, tiles_m - band * g);
+                const int64_t bs = band * g * tiles_n, be = bs + h * tiles_n;
+                const int64_t u = t - bs, v = std::min(t1, be) - bs;  // [u, v) in the band
+                rows += (v - u) >= h ? h : (v - u);
+                col_lo = std::min(col_lo, u / h);
+                col_hi = std::max(col_hi, (v - 1) / h);
+                t = bs + v;
+            }
+            cost += rows * bm + (col_hi - col_lo + 1) * bn;
+            a = b;
+        }
+    }
+    return cost;
+}
+
+int tile_group(const GemmParams& p, const TileCfg& t, int64_t ntiles, int forced) {
+    const int tiles_m = (p.M + t.bm - 1) / t.bm;
+    const int tiles_n = (p.N + t.bn - 1) / t.bn;
+    if (forced < 0) return 1;
+    if (forced > 0) return std::min(forced, tiles_m);
+    if ((ntiles * p.splits) / 8 < 2) return 1;
+    int best = 1;
+    int64_t best_cost = xcd_panel_cost(tiles_m, tiles_n, p.splits, 1, t.bm, t.bn);
+    for (int g = 2; g <= tiles_m && g <= 64; g = g < 8 ? g + 1 : g * 2) {
+        const int64_t c = xcd_panel_cost(tiles_m, tiles_n, p.splits, g, t.bm, t.bn);
+        if (c < best_cost) {
+            best_cost = c;
+            best = g;
+        }
+    }
+    return best;
+}
+
 int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmode,
                 float* workspace, size_t workspace_bytes, const GemmTune* tune) {
     static const GemmTune kAuto;
@@ -2075,12 +2150,13 @@ int gemm_launch(hipStream_t stream, GemmParams p, int amode, int bmode, int cmod
         t.pg = 2;
     if (tn.pg && !t.bl) t.pg = tn.pg;
     int64_t ntiles = (int64_t)((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
-    if (ntiles > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
+    if (ntiles * p.splits > 0x7fffffff) return fail(SHP_ERR_SHAPE, "gemm: too many tiles");
     // in-kernel split-K fixup where the tile counters fit and few splits share a tile (the last
     // split sums them serially: with 16 splits of the M = 32 ResNet FC it is 2.5x slower than
     // the separate reduction pass); the separate pass otherwise
     p.fixup = pl.splits > 1 && pl.splits <= 4 && fix_ok &&
               ntiles * nbatch <= (int64_t)(kSplitCounterBytes / sizeof(int));
+    p.group_m = tile_group(p, t, ntiles, tn.group);
     dim3 grid((unsigned)ntiles, (unsigned)p.splits, (unsigned)nbatch);
     int rc = t.bl    ? dispatch_bl(stream, p, amode, bmode, t, grid)
              : t.dma ? launch_dma(stream, p, amode, t.bn, grid)

@@ -322,7 +322,7 @@ int shp_workspace_info(shp_ctx* ctx, void** dptr, uint64_t* bytes) {
 
 // Force parts of the dense-kernel planner's choice for launches on this context only
 // (0 restores the automatic choice): gemm_tile, gemm_bk, gemm_splits, gemm_dma, gemm_pg,
-// gemm_table, gemm_bl, gemm_sk, gemm_stem, dw_tile.
+// gemm_table, gemm_bl, gemm_sk, gemm_stem, gemm_group, dw_tile.
 int shp_tune(shp_ctx* ctx, const char* key, int value) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_tune: null ctx");
     shp::GemmTune& t = reinterpret_cast<Ctx*>(ctx)->tune;
@@ -337,6 +337,7 @@ int shp_tune(shp_ctx* ctx, const char* key, int value) {
     else if (k == "gemm_sk") t.sk = value;
     else if (k == "gemm_stem") t.stem = value;
     else if (k == "dw_tile") t.dw = value;
+    else if (k == "gemm_group") t.group = value;
     else return fail(SHP_ERR_INVALID, "shp_tune: unknown key '" + k + "'");
     return SHP_OK;
 }

@@ -6,7 +6,8 @@
 Every pass launches the graph eagerly (one dispatch per op, in graph order), so a kernel trace
 or a counter collection sees each op as its own dispatch; `--graph` replays a hipGraph
 capture instead.  `--copy-calibration-mb N` ends with one N MiB `reshape` copy (N MiB read and
-N MiB written), against which HBM byte counters are scaled.  The op list (kernel, label,
+N MiB written), against which HBM byte counters are scaled.  `--tune KEY=VALUE` applies a
+planner override (shp_tune) to the run's context.  The op list (kernel, label,
 algorithmic bytes and FLOPs per op) is written as JSON with `--ops-json`, so a trace can be
 matched op by op.
 """
@@ -58,8 +59,13 @@ def main(argv=None) -> int:
     ap.add_argument("--graph", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     ap.add_argument("--ops-json")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="planner override for this run's context (shp_tune), e.g. gemm_group=-1")
     a = ap.parse_args(argv)
     with Context("any") as ctx:
+        for kv in a.tune:
+            k, v = kv.split("=", 1)
+            ctx.tune(k, int(v))
         with Model(ctx, a.arch, a.batch, a.seq, seed=2) as m:
             ops = m.ops()
             info = {}

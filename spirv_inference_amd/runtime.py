@@ -174,6 +174,10 @@ class Context:
         return KernelOutput(out, info.device_name.decode(), info.vendor_id, info.device_id,
                             info.elapsed_ms)
 
+    def tune(self, key: str, value: int) -> None:
+        """Planner override for this context's dense launches (shp_tune; 0 = automatic)."""
+        check(lib().shp_tune(self.handle, key.encode(), int(value)), "shp_tune")
+
     # -- timing (KernelOutput.elapsed_ms per launch, accumulated per kernel name)
     def timing(self, enable: bool) -> None:
         check(lib().shp_timing_enable(self.handle, 1 if enable else 0), "shp_timing_enable")

@@ -594,7 +594,15 @@ class TfliteExecutor:
       CONCATENATION      -> hlo_concatenate_into per input (:710-794)
       L2_NORMALIZATION   -> l2_normalization (on-device norm; :795-836 computes it on the CPU)
     A fused activation runs in the producing kernel's epilogue where it has one, else as a
-    unary launch.  Anything else raises, like the reference's scheduler.
+    unary launch.  A CONV_2D without activation whose output is read only by an ADD of an
+    equal-sized tensor computed earlier (a residual connection) runs as one conv2d_nhwc launch
+    with that tensor as the epilogue's residual and the ADD's activation; the ADD then
+    dispatches nothing.  Anything else raises, like the reference's scheduler.
+
+    run(graph=True) replays the launch sequence from one hipGraph: the first such call runs
+    eagerly if nothing ran yet (so every buffer, packed weight and split-K workspace exists),
+    then captures the sequence once; later calls replay it.  Tensors keep their device
+    buffers across runs, so set_input() between replays feeds the graph.
     """
 
     def __init__(self, ctx, model: TfliteModel):
@@ -614,6 +622,9 @@ class TfliteExecutor:
         self.packed: Dict[Tuple[int, int], object] = {}
         self.op_log: List[dict] = []
         self._check_aliases()
+        self.residual_adds = self._find_residual_adds()
+        self._graph = None
+        self._warm = False
 
     def _check_aliases(self) -> None:
         """The view ops' rules (scheduler.rs:230-249), checked before anything runs: Cast
@@ -635,6 +646,38 @@ class TfliteExecutor:
             if self._elems(src) != self._elems(dst):
                 raise ValueError(f"operator {op.index} {op.builtin} element count changed from "
                                  f"{self._elems(src)} to {self._elems(dst)}")
+
+    def _find_residual_adds(self) -> Dict[int, Tuple[int, int]]:
+        """{conv operator index: (add operator index, residual tensor)} for every CONV_2D
+        that can take the ADD after it as its epilogue (see the class docstring)."""
+        pos = {oi: k for k, oi in enumerate(self.order)}
+        producer, readers = {}, {}
+        for op in self.model.operators:
+            for t in op.outputs:
+                producer[t] = op.index
+            for t in op.inputs:
+                readers.setdefault(t, []).append(op.index)
+        out = {}
+        for op in self.model.operators:
+            if op.builtin != "CONV_2D" or decode_options(op)["fused_activation"] != "none":
+                continue
+            t = op.outputs[0]
+            r = readers.get(t, [])
+            if len(r) != 1 or t in self.model.outputs:
+                continue
+            add = self.model.operators[r[0]]
+            if add.builtin != "ADD" or len(add.inputs) != 2 or add.inputs.count(t) != 1:
+                continue
+            other = add.inputs[1] if add.inputs[0] == t else add.inputs[0]
+            if self._elems(other) != self._elems(t) or self._elems(add.outputs[0]) != self._elems(t):
+                continue
+            if decode_options(add).get("fused_activation", "none") not in ("none", "relu", "relu6", "tanh"):
+                continue
+            p = producer.get(other)
+            if p is not None and pos.get(p, 1 << 30) > pos[op.index]:
+                continue  # the residual must exist when the convolution runs
+            out[op.index] = (add.index, other)
+        return out
 
     # -- helpers
     def _shape(self, idx: int) -> List[int]:
@@ -699,13 +742,32 @@ class TfliteExecutor:
         t = self._alloc(idx)
         t.upload(v)
 
-    def run(self) -> None:
+    def run(self, graph: bool = False) -> None:
+        if graph and self._graph is not None:
+            self._graph.launch()
+            return
+        if graph and self._warm:
+            self.ctx.capture_begin()
+            try:
+                self._run_ops()
+            finally:
+                self._graph = self.ctx.capture_end()
+            self._graph.launch()
+            return
+        self._run_ops()
+        self._warm = True
+
+    def _run_ops(self) -> None:
         self.op_log = []  # the dispatches of this run
+        fused_adds = {a: c for c, (a, _) in self.residual_adds.items()}
         for oi in self.order:
             op = self.model.operators[oi]
             self.op_log.append({"index": op.index, "op": op.builtin,
                                 "options": decode_options(op), "inputs": op.inputs,
                                 "outputs": op.outputs, "dispatches": []})
+            if op.index in fused_adds:
+                self.op_log[-1]["fused_into"] = fused_adds[op.index]
+                continue
             self._run_op(op, self.op_log[-1]["options"])
 
     def output(self, index: int = 0) -> np.ndarray:
@@ -715,9 +777,13 @@ class TfliteExecutor:
         return self._get(idx).download()
 
     def close(self) -> None:
+        if self._graph is not None:
+            self._graph.destroy()
+            self._graph = None
         for t in self.owned:
             t.free()
         self.owned, self.dev, self.packed = [], {}, {}
+        self._warm = False
 
     def _run_op(self, op: Operator, o: dict) -> None:
         b = op.builtin
@@ -741,15 +807,22 @@ class TfliteExecutor:
             pt, pl = (_same_pads(ih, iw, oh, ow, kh, kw, sh, sw) if o["padding"] == "same"
                       else (0, 0))
             w = self._pack(ins[1], ins[2] if len(ins) > 2 else -1, oc)
-            y = self._alloc(out_idx)
             act = o["fused_activation"]
             fused = act if act in ("none", "relu", "relu6", "tanh") else None
             if fused is None:
                 raise ValueError(f"operator {op.index}: fused activation {act} not supported")
+            residual = None
+            if op.index in self.residual_adds:  # conv + bias + residual, then the ADD's act
+                add_i, r_idx = self.residual_adds[op.index]
+                add = self.model.operators[add_i]
+                out_idx = add.outputs[0]
+                residual = self._get(r_idx)
+                fused = decode_options(add).get("fused_activation", "none")
+            y = self._alloc(out_idx)
             self._launch("conv2d_nhwc", self._get(ins[0]), w, y,
                          [n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw,
                           1 if o["padding"] == "same" else 0, pt, pl, n * oh * ow * oc],
-                         act=fused)
+                         act=fused, residual=residual)
             return
         if b == "DEPTHWISE_CONV_2D":
             n, ih, iw, c = self._shape(ins[0])

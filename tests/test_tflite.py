@@ -195,3 +195,59 @@ def test_cast_only_float32_to_float32():
     m = _alias_model("CAST", [1, 8], [1, 8], in_type=2)  # Int32 -> Float32
     with pytest.raises(ValueError, match="Cast only supports Float32->Float32, got Int32->Float32"):
         T.TfliteExecutor(None, m)
+
+
+def _residual_model(conv_act=0, add_act=0, extra_reader=False, late_residual=False):
+    """x -> CONV_2D (1x1) -> y; ADD(y, x) -> z (a residual connection), with variants that
+    must not fuse: an activation on the convolution, a second reader of y, a residual that
+    is computed after the convolution."""
+    w = T.TfliteWriter()
+    x = w.tensor("x", [1, 4, 4, 3])
+    k = w.tensor("k", [3, 1, 1, 3], np.ones(9, np.float32))
+    y = w.tensor("y", [1, 4, 4, 3])
+    z = w.tensor("z", [1, 4, 4, 3])
+    w.inputs, w.outputs = [x], [z]
+    conv_opts = {0: ("b", 0), 1: ("i", 1), 2: ("i", 1), 3: ("b", conv_act)}
+    if late_residual:
+        r = w.tensor("r", [1, 4, 4, 3])
+        w.op("CONV_2D", [x, k, -1], [y], "Conv2DOptions", conv_opts)
+        w.op("ABS", [x], [r])
+        w.op("ADD", [y, r], [z], "AddOptions", {0: ("b", add_act)})
+    else:
+        w.op("CONV_2D", [x, k, -1], [y], "Conv2DOptions", conv_opts)
+        w.op("ADD", [y, x], [z], "AddOptions", {0: ("b", add_act)})
+    if extra_reader:
+        q = w.tensor("q", [1, 4, 4, 3])
+        w.op("NEG", [y], [q])
+        w.outputs.append(q)
+    return T.parse_model(w.finish())
+
+
+class _NoDevice:
+    """TfliteExecutor's constructor touches no device; its fusion analysis is host logic."""
+
+
+@pytest.mark.parametrize("variant,fused", [({}, True), ({"add_act": 3}, True),
+                                           ({"conv_act": 1}, False),
+                                           ({"extra_reader": True}, False)])
+def test_executor_fuses_residual_add_into_conv(variant, fused):
+    m = _residual_model(**variant)
+    ex = T.TfliteExecutor(_NoDevice(), m)
+    conv = next(o.index for o in m.operators if o.builtin == "CONV_2D")
+    add = next(o.index for o in m.operators if o.builtin == "ADD")
+    if fused:
+        assert ex.residual_adds == {conv: (add, 0)}
+    else:
+        assert ex.residual_adds == {}
+
+
+def test_executor_keeps_add_when_residual_comes_later():
+    m = _residual_model(late_residual=True)
+    order = T.topological_order(m)
+    ex = T.TfliteExecutor(_NoDevice(), m)
+    conv = next(o.index for o in m.operators if o.builtin == "CONV_2D")
+    absop = next(o.index for o in m.operators if o.builtin == "ABS")
+    if order.index(absop) > order.index(conv):
+        assert ex.residual_adds == {}
+    else:
+        assert conv in ex.residual_adds

@@ -2,9 +2,9 @@
 against a float64 numpy restatement of the TFLite ops (small graphs) and against the resident
 model graph the file was exported from.
 
-Gates: per-graph outputs within 1e-4 abs + 1e-4 rel (BASELINE.json per-op tolerance), the
-exported MobileNetV2 bit-identical to the graph it came from except for the residual adds
-(one rounding apart), identical top-1.
+Gates: per-graph outputs within 1e-4 abs + 1e-4 rel (BASELINE.json per-op tolerance); the
+exported MobileNetV2 and EfficientNet-Lite0 bit-identical to the graphs they came from,
+eagerly and from the executor's hipGraph.
 """
 import json
 import subprocess
@@ -129,9 +129,12 @@ def test_small_cnn_graph(ctx):
     ref = e / e.sum()  # softmax1000 over every element of the output, as the reference
     assert_close(got, ref.reshape(-1), 1e-4, 1e-4, "small cnn probs")
     kernels = [d["kernel"] for op in rep["ops"] for d in op["dispatches"]]
-    assert kernels == ["conv2d_nhwc", "depthwise_conv2d_nhwc", "conv2d_nhwc", "add",
+    # the residual ADD runs in the second convolution's epilogue
+    assert kernels == ["conv2d_nhwc", "depthwise_conv2d_nhwc", "conv2d_nhwc",
                        "hlo_reduce_window_rank4", "hlo_concatenate_into", "hlo_concatenate_into",
                        "global_avg_pool_nhwc", "fully_connected", "softmax1000"]
+    add = next(op for op in rep["ops"] if op["op"] == "ADD")
+    assert add["dispatches"] == [] and "fused_into" in add
     # one executor over several inputs: every tensor keeps its buffer, results repeat
     ex = T.TfliteExecutor(ctx, m)
     try:
@@ -151,27 +154,55 @@ def test_small_cnn_graph(ctx):
         ex.close()
 
 
-def test_mobilenet_v2_export_roundtrip(ctx):
-    """A resident MobileNetV2 graph exported to TFL3, parsed back and run by the executor
-    equals the graph's own run: every op is the same kernel on the same weights, except that
-    a residual the graph fuses into the projection convolution becomes CONV_2D + ADD."""
+@pytest.mark.parametrize("arch,batch,adds", [("mobilenet_v2", 1, 10),
+                                             ("efficientnet_lite0", 8, 9)])
+def test_export_roundtrip_and_graph_replay(ctx, arch, batch, adds):
+    """A resident model graph exported to TFL3, parsed back and run by the executor equals
+    the graph's own run bit for bit: every op is the same kernel with the same push vector
+    on the same weights (the executor folds each CONV_2D + ADD residual back into one
+    epilogue launch, as the graph has it).  Replays of the executor's hipGraph equal its
+    eager run, with a new input set between replays."""
     from spirv_inference_amd.models import Model
-    with Model(ctx, "mobilenet_v2", 1, seed=2) as mdl:
+    with Model(ctx, arch, batch, seed=2) as mdl:
         mdl.run()
         ctx.sync()
         probs = mdl.output(0).download()
-        logits = mdl.output(1).download()
         x = mdl.input(0).download()
+        n_graph_ops = len(mdl.ops())
         data = T.model_to_tflite(mdl)
     m = T.parse_model(data)
     assert not m.unsupported_ops and not m.quantized_tensors
-    assert m.op_histogram["ADD"] == 10 and m.op_histogram["DEPTHWISE_CONV_2D"] == 17
-    print(f"[gpu] tflite mobilenet_v2 export: {len(data)} bytes, {len(m.operators)} ops",
+    assert m.op_histogram["ADD"] == adds
+    print(f"[gpu] tflite {arch} b{batch} export: {len(data)} bytes, {len(m.operators)} ops",
           flush=True)
+    ex = T.TfliteExecutor(ctx, m)
+    try:
+        assert len(ex.residual_adds) == adds
+        ex.set_input(x)
+        ex.run()
+        ctx.sync()
+        eager = ex.output()
+        assert sum(len(o["dispatches"]) for o in ex.op_log) == n_graph_ops
+        assert eager.tobytes() == probs.tobytes(), np.abs(eager - probs).max()
+        x2 = (x[::-1] * 0.5).astype(np.float32).copy()
+        for rep in range(3):
+            ex.set_input(x if rep % 2 == 0 else x2)
+            ex.run(graph=True)
+            ctx.sync()
+            got = ex.output()
+            if rep % 2 == 0:
+                assert got.tobytes() == eager.tobytes(), f"replay {rep}"
+            else:
+                other = got
+        ex.set_input(x2)
+        ex.run()  # eager on the second input equals its replay
+        ctx.sync()
+        assert ex.output().tobytes() == other.tobytes()
+    finally:
+        ex.close()
     rep, got = T.run_model(ctx, m, x)
-    assert_close(got, probs, 1e-6, 1e-4, "exported mobilenet_v2 probs")
-    assert int(np.argmax(got)) == int(np.argmax(probs)) == int(np.argmax(logits))
-    assert rep["top1"]["model_class"] == int(np.argmax(probs))
+    assert got.tobytes() == probs.tobytes()
+    assert rep["top1"] == T.top1(probs)
 
 
 def test_tflite_run_cli(tmp_path):
