@@ -70,6 +70,30 @@ __device__ __forceinline__ void st_coh4(float* p, float4 v) {
                                   ((unsigned long long)__float_as_uint(v.w) << 32),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+
+// Raw dword buffer resource word 3 for gfx9-family devices.
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base, int64_t elems) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(elems * 4), kBufferWord3);
+}
+
+// The same device-coherent 16-byte store and load as single buffer instructions with the
+// agent-scope coherence bit (sc1), the bit the 8-byte agent-scope atomics above carry: one
+// request per 16 bytes instead of two.  Byte offsets are 32-bit (ranges < 2 GiB).
+constexpr int kCohSc1 = 16;  // cache-policy operand: sc1
+__device__ __forceinline__ void st_coh16(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4 v) {
+    const f4v x = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, x), r, byte_off, 0, kCohSc1);
+}
+__device__ __forceinline__ float4 ld_coh16(__amdgpu_buffer_rsrc_t r, unsigned byte_off,
+                                           unsigned soff) {
+    const f4v x = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, soff, kCohSc1));
+    return make_float4(x.x, x.y, x.z, x.w);
+}
+
 __device__ __forceinline__ float4 ld_coh4(const float* p) {
     SHP_GLOBAL unsigned long long* q = (SHP_GLOBAL unsigned long long*)p;
     const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -157,6 +181,10 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
                           (p.N & 3) == 0 && (((uintptr_t)C) & 15) == 0 &&
                           (!p.bias || (((uintptr_t)p.bias) & 15) == 0) &&
                           (!R || (((uintptr_t)R) & 15) == 0));
+    // fixup partials as 16-byte coherent buffer accesses while every split's slice fits the
+    // 32-bit offsets (all of them: < 2 GiB together), else as 8-byte coherent atomics
+    const bool coh16 = P && p.fixup && (int64_t)nsplit * nbatch * p.M * p.N < (1ll << 29);
+    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(P ? P : p.c, (int64_t)p.M * p.N);
     constexpr int TPR = BN / 4, RPP = 256 / TPR;
     const int cl4 = (tid % TPR) * 4;
     const int col4 = n0 + cl4;
@@ -185,7 +213,8 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
                 if (row >= p.M || col4 >= p.N) continue;
                 float4 v = *reinterpret_cast<const float4*>(&Cs[rl * CS + cl4]);
                 if (P) {
-                    if (p.fixup) st_coh4(P + (int64_t)row * p.N + col4, v);
+                    if (coh16) st_coh16(prs, (unsigned)(((int64_t)row * p.N + col4) * 4), v);
+                    else if (p.fixup) st_coh4(P + (int64_t)row * p.N + col4, v);
                     else *reinterpret_cast<float4*>(P + (int64_t)row * p.N + col4) = v;
                     continue;
                 }
@@ -241,6 +270,7 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
         if (!*last) return;
         const float* P0 = p.partial + (int64_t)bz * p.M * p.N;
         const int64_t sstride = (int64_t)nbatch * p.M * p.N;
+        const __amdgpu_buffer_rsrc_t p0rs = buffer_rsrc(P0, (int64_t)nsplit * sstride);
         if (p.bias && col4 < p.N) bv = *reinterpret_cast<const float4*>(p.bias + col4);
         for (int i = 0; i < BM / RPP; ++i) {
             const int row = m0 + tid / TPR + RPP * i;
@@ -248,7 +278,9 @@ __device__ __attribute__((always_inline)) inline void gemm_epilogue(
             const float* pp = P0 + (int64_t)row * p.N + col4;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int s = 0; s < nsplit; ++s) {
-                const float4 q = ld_coh4(pp + s * sstride);
+                const float4 q = coh16 ? ld_coh16(p0rs, (unsigned)(((int64_t)row * p.N + col4) * 4),
+                                                  (unsigned)(s * sstride * 4))
+                                       : ld_coh4(pp + s * sstride);
                 v.x += q.x;
                 v.y += q.y;
                 v.z += q.z;
@@ -631,16 +663,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 // one load of the tile after it (two tiles in flight), and the next step's fragments are read
 // before its MFMAs, so LDS and global latency overlap the MFMA stream instead of sitting
 // between dependent MFMAs.
-typedef float f4v __attribute__((ext_vector_type(4)));
-
-// Raw dword buffer resource word 3 for gfx9-family devices.
-constexpr int kBufferWord3 = 0x00020000;
 // A byte offset beyond every operand range (the host keeps ranges <= 2 GiB): loads return 0.
 constexpr unsigned kOobOffset = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* base, int64_t elems) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(elems * 4), kBufferWord3);
-}
 
 __device__ __forceinline__ f4v buffer_load4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
     return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
