@@ -377,3 +377,53 @@ def test_sin_cos_within_one_ulp_of_float64(orc, name, ref):
     else:
         assert (sp[:2] == 1.0).all()
     assert np.isnan(sp[2:]).all()
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "relu6", "leaky", "sigmoid", "tanh", "silu",
+                                 "gelu_erf"])
+def test_bias_act_vs_float64(orc, act):
+    """bias_act (the standalone epilogue: x + bias[i % period] + residual, then the
+    activation) against float64 numpy."""
+    x, b, r = rnd(4, 100), rnd(100), rnd(4, 100)
+    y = orc.run("bias_act", x, None, 400, [400, 100], bias=b, residual=r, act=act, alpha=0.2)
+    ref = _act_ref(x.astype(np.float64) + b + r, act, 0.2)
+    assert_close(y, ref, 1e-6, 1e-6, f"bias_act {act}")
+
+
+@pytest.mark.parametrize("name,ref", [("logistic", lambda v: 1.0 / (1.0 + np.exp(-v))),
+                                      ("silu", lambda v: v / (1.0 + np.exp(-v)))])
+def test_logistic_and_silu_kernels_vs_float64(orc, name, ref):
+    """The unary kernels `logistic` (TFLite's name for sigmoid.comp) and `silu` over a wide
+    range, including the saturated tails."""
+    x = np.concatenate([rnd(1000, scale=4.0), np.float32([-90, -30, -1e-3, 0, 1e-3, 30, 90])])
+    y = orc.run(name, x, None, x.size, [x.size])
+    assert_close(y, ref(x.astype(np.float64)), 1e-6, 1e-6, name)
+
+
+def test_argmax_rows_first_maximum(orc):
+    """argmax_rows: per row the index of the first maximum (numpy's rule, lowest index on
+    ties), stored as int32 bits."""
+    rows, cols = 6, 1000
+    x = rnd(rows, cols)
+    x[1, [10, 500, 999]] = 9.0    # a three-way tie: the first index wins
+    x[2, :] = -1.0                # every column tied
+    x[3, 999] = 50.0              # maximum in the last column
+    x[4, 0] = 50.0                # and in the first
+    y = orc.run("argmax_rows", x, None, rows, [rows, cols]).view(np.int32)
+    assert list(y) == list(np.argmax(x, axis=1))
+    assert list(y[1:5]) == [10, 0, 999, 0]
+
+
+def test_compare_is_tensor_rs_comparator(orc):
+    """orc_compare restates tflite_loader/src/tensor.rs:28-54: a mismatch is |a - e| > eps (a
+    difference equal to eps is not one), the relative error divides by max(|e|, 1e-30), and
+    a length difference counts as that many mismatches; the maxima cover the common prefix."""
+    e = np.float32([1.0, -2.0, 0.0, 4.0, 5.0])
+    a = np.float32([1.0, -2.5, 1e-3, 4.0 + 0.25, 5.0])
+    mm, ma, mr = orc.compare(a, e, 0.25)
+    assert mm == 1                                    # only -2.5 (0.5 > eps); 4.25 sits at eps
+    assert ma == np.float32(0.5)
+    assert mr == np.float32(np.float32(1e-3) / np.float32(1e-30))
+    mm2, _, _ = orc.compare(a[:3], e, 0.25)           # two missing values
+    assert mm2 == 1 + 2
+    assert orc.compare(e, e, 0.0)[0] == 0
