@@ -130,6 +130,15 @@ int shp_launch_static(shp_ctx* ctx, const char* kernel, const void* in0, const v
                       void* out, const int32_t* push, size_t n_push, uint64_t out_elems,
                       const shp_epilogue* epi);
 
+/* Plan query of the fused MBConv kernel inverted_residual_nhwc (one launch for the three
+ * operators scheduler.rs:321-548 dispatches for a MobileNetV2 / EfficientNet-Lite block:
+ * 1x1 CONV_2D, DEPTHWISE_CONV_2D, 1x1 CONV_2D + residual ADD).  Host-only, no device needed.
+ * out8 = {tile rows, tile columns, expanded-channel splits, output-channel splits, LDS bytes,
+ * workgroups, projection blocks per wavefront, 1 if one launch is expected to beat the three
+ * operators}.  Returns SHP_ERR_UNSUPPORTED for blocks the kernel does not take (a front end
+ * then dispatches the three operators). */
+int shp_block_plan(const int32_t* push, size_t n_push, int32_t* out8);
+
 /* Host-to-host synchronous call with the semantics of
  * run_kernel(device_selector, &KernelRun) (source/tflite_loader/src/vulkan.rs:42-44):
  * upload in0[n0], in1[n1], dispatch, wait, download out[n_out].  grid_hint (the

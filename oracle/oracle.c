@@ -714,7 +714,7 @@ static const char* kNames[] = {
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
     "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
     "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
-    "hlo_reduce", "hlo_strided_copy", "attention_fused", "nan_count"};
+    "hlo_reduce", "hlo_strided_copy", "attention_fused", "nan_count", "inverted_residual_nhwc"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -898,6 +898,45 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
         int nhwc = !strcmp(name, "conv2d_nhwc");
         k_conv2d(in0, in1, out, push, nhwc);
         epilogue(out, n_out, 0, NULL, residual, act, alpha);
+        return 0;
+    }
+    if (!strcmp(name, "inverted_residual_nhwc")) {
+        /* An MBConv block as the TFLite scheduler dispatches it, three operators in order
+         * (scheduler.rs:321-427 CONV_2D, :429-548 DEPTHWISE_CONV_2D, then the projection
+         * CONV_2D and the residual ADD): the loops of conv2d_nhwc (1x1) and
+         * depthwise_conv2d_nhwc above on the operators' own weight tensors, which the packed
+         * in1 holds back to back.  push {n, cin, h, w, ce, cout, oh, ow, k, s, pt, pl,
+         * expand, act_e, act_d, total}; residual and act apply to the projection. */
+        NEED(16);
+        const int n = push[0], cin = push[1], h = push[2], w = push[3], ce = push[4],
+                  cout = push[5], oh = push[6], ow = push[7], k = push[8], st = push[9],
+                  pt = push[10], pl = push[11], expand = push[12], act_e = push[13],
+                  act_d = push[14];
+        TOTAL((int64_t)n * oh * ow * cout);
+        if (!expand && ce != cin) return orc_fail(-4, "inverted_residual_nhwc: ce != cin");
+        const float* wp = in1;
+        const float* e = in0;
+        float* ebuf = NULL;
+        if (expand) {
+            const size_t ne = (size_t)n * h * w * ce;
+            ebuf = (float*)malloc(sizeof(float) * ne);
+            const int32_t qe[15] = {n, cin, h, w, ce, h, w, 1, 1, 1, 1, 1, 0, 0, (int32_t)ne};
+            k_conv2d(in0, wp, ebuf, qe, 1);
+            epilogue(ebuf, ne, 0, NULL, NULL, act_e, alpha);
+            e = ebuf;
+            wp += (size_t)ce * cin + ce;
+        }
+        const size_t nd = (size_t)n * oh * ow * ce;
+        float* dbuf = (float*)malloc(sizeof(float) * nd);
+        const int32_t qd[16] = {n, ce, h, w, oh, ow, k, k, st, st, 1, pt, pl, 1, 1, (int32_t)nd};
+        k_depthwise(e, wp, dbuf, qd, 1);
+        epilogue(dbuf, nd, 0, NULL, NULL, act_d, alpha);
+        wp += (size_t)k * k * ce + ce;
+        const int32_t qp[15] = {n, ce, oh, ow, cout, oh, ow, 1, 1, 1, 1, 1, 0, 0, (int32_t)n_out};
+        k_conv2d(dbuf, wp, out, qp, 1);
+        epilogue(out, n_out, 0, NULL, residual, act, alpha);
+        free(ebuf);
+        free(dbuf);
         return 0;
     }
     if (!strcmp(name, "depthwise_conv2d") || !strcmp(name, "depthwise_conv2d_nhwc")) {

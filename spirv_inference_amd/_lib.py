@@ -86,6 +86,7 @@ SIGNATURES = [
     ("shp_launch_static", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.POINTER(C.c_int32), C.c_size_t, C.c_uint64,
                                     C.POINTER(Epilogue)]),
+    ("shp_block_plan", C.c_int, [C.POINTER(C.c_int32), C.c_size_t, C.POINTER(C.c_int32)]),
     ("shp_run_kernel", C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                  C.c_size_t, C.c_void_p, C.c_size_t, C.POINTER(C.c_int32),
                                  C.c_size_t, C.c_uint32, C.POINTER(RunInfo)]),

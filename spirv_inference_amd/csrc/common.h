@@ -37,6 +37,13 @@ int fail(int code, const std::string& msg);
 struct GemmTune {
     int tile = 0, bk = 0, splits = 0, dma = 0, pg = 0, table = 0, dw = 0, bl = 0, sk = 0, stem = 0;
     int group = 0;  // tile-row band of the tile order: 0 automatic, -1 row major, k > 0 forced
+    // inverted_residual_nhwc plan: output tile rows x columns, expanded-channel splits and
+    // output-channel splits (0: the planner's choice)
+    int ir_th = 0, ir_tw = 0, ir_s = 0, ir_j = 0;
+    // model graphs: MBConv blocks as one inverted_residual_nhwc launch where it is expected
+    // to pay (0), always (1), or as the three operators the TFLite scheduler dispatches (-1);
+    // read when a model is built
+    int ir_fuse = 0;
 };
 
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.
@@ -76,6 +83,8 @@ extern KernelEntry kHloOpKernels[];
 extern const int kHloOpKernelCount;
 extern KernelEntry kDecodeKernels[];
 extern const int kDecodeKernelCount;
+extern KernelEntry kBlockKernels[];
+extern const int kBlockKernelCount;
 
 const KernelEntry* find_kernel(const char* name);
 
@@ -88,6 +97,11 @@ int launch_kernel(hipStream_t stream, const char* name, const void* in0, const v
 // Split-K workspace a dense kernel would ask for with this push vector (0 if none).
 size_t gemm_workspace_for_kernel(const char* name, const int32_t* push, size_t n_push,
                                  const GemmTune* tune);
+// The same for the fused block kernel inverted_residual_nhwc (kernels_block.hip).
+size_t block_workspace_for_kernel(const int32_t* push, size_t n_push, const GemmTune* tune);
+// Whether that kernel takes this push vector and is expected to beat the block's three
+// operators (measured verdicts for the benchmark configs' blocks, a rule elsewhere).
+bool block_fusion_pays(const int32_t* push, size_t n_push);
 
 // Counter-based RNG fill (kernels_elementwise.hip).
 int fill_random(hipStream_t stream, float* p, uint64_t n, uint64_t seed, uint64_t tensor_id,

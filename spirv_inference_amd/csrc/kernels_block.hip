@@ -1,0 +1,836 @@
+// inverted_residual_nhwc: a MobileNetV2 / EfficientNet-Lite inverted-residual (MBConv) block
+// in one launch.
+//
+// The reference runs the block as three TFLite operators, one dispatch and one host round
+// trip each (source/tflite_loader/src/scheduler.rs:321-427 CONV_2D, :429-548
+// DEPTHWISE_CONV_2D, then the projection CONV_2D with the residual ADD):
+//   E = act_e(x . We + be)               1x1 expand    (kernels/conv2d/glsl/conv2d.comp:26-50)
+//   D = act_d(depthwise_k,s(E) + bd)     depthwise     (depthwise_conv2d.comp:27-49, SAME pad)
+//   y = act_o(D . Wp + bp [+ x])         1x1 project + residual
+// A workgroup here owns an output tile of TH x TW pixels of one image and a slice of the
+// output channels.  It stages the input patch that the tile's depthwise windows cover (the
+// halo) in LDS once, then walks the expanded channels 16 at a time:
+//   1. expand: the halo patch times 16 columns of We on the fp32 matrix cores
+//      (v_mfma_f32_16x16x4_f32, operands from LDS), + bias, activation, and zero where the
+//      halo pixel lies outside the image (the depthwise's SAME padding of E);
+//   2. depthwise: the k x k taps of those 16 channels from LDS, + bias, activation;
+//   3. project: those 16 channels times their 16 rows of Wp, accumulated in MFMA registers.
+// E and D never leave the CU: the block reads x and the weights and writes y, where the
+// three-operator form also writes and reads back the expanded tensor (the block's largest)
+// and the depthwise output, and pays two more launches.
+//
+// Where the tiles alone cannot fill the GPU (7x7 and 14x14 maps at batch 1) the expanded
+// channels are split over S workgroups per tile (each projects its own channel range) and
+// the output channels over J.  The S partial projections of a tile go to the context
+// workspace with device-coherent stores; the workgroup that completes the tile last sums
+// them in split order (so the result does not depend on arrival order), applies bias,
+// residual and activation, and resets the tile's arrival counter to zero.
+//
+// Packed weights (in1), the three operators' own tensors back to back:
+//   [We: ce x cin (OHWI 1x1) | be: ce]  (only with expand = 1)
+//   [Wd: k x k x ce ([KH][KW][C]) | bd: ce] [Wp: cout x ce (OHWI 1x1) | bp: cout]
+// push {n, cin, h, w, ce, cout, oh, ow, k, s, pt, pl, expand, act_e, act_d, total};
+// the epilogue's residual and activation apply to y (its bias slot must be empty).
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "coherent.h"
+#include "common.h"
+#include "gemm.h"
+
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int CC = 32;       // expanded channels per chunk (two 16-column MFMA blocks)
+constexpr int ES = CC + 1;   // LDS row stride (floats) of the expanded chunk
+constexpr int DS = CC + 4;   // of the depthwise chunk: 16-byte rows, 4 banks apart
+constexpr int WPS = CC + 4;  // of the projection weight chunk
+constexpr int NPF = 12;      // float4 weight loads per thread and chunk, at most
+constexpr int kMaxLds = 160 * 1024;
+
+struct IrArgs {
+    const float* x;
+    const float* w;
+    float* y;
+    const float* res;
+    float* partial;
+    int* counters;
+    int n, h, w_, cin, ce, cout, oh, ow, pt, pl;
+    int expand, act_e, act_d, act_o;
+    float alpha;
+    int th, tw, tiles_y, tiles_x;  // output tile and the tile grid of one image
+    int hw, hp, hpb;               // halo columns, halo pixels, 16-row blocks of them
+    int cin16, xs, wsx;            // cin rounded up to 16; LDS row strides of x and We
+    int nchunk, cpw, S;            // 32-channel chunks of ce (the last may hold 16),
+                                   // chunks per split, splits
+    int J, coj, ob, pb;            // output-channel splits, channels per split (16 * ob),
+                                   // 16-row blocks of the output tile
+    int o_x, o_w, o_be, o_wd, o_bd, o_e, o_d, o_wp, o_hv, o_flag;  // LDS offsets (floats)
+    int w_we, w_be, w_wd, w_bd, w_wp, w_bp;                        // packed-weight offsets
+    // ceil(2^32 / d) for the divisors cin / 4, cin16 / 4, hw and tw: n / d = umulhi(n, m)
+    // exactly for n * d < 2^32
+    unsigned m_cin4, m_c4n, m_hw, m_tw;
+};
+
+__device__ __forceinline__ int udiv(int n, unsigned m) {
+    return m ? (int)__umulhi((unsigned)n, m) : n;  // m = 0 stands for d = 1
+}
+
+// The idx-th float4 of one chunk's weights: We rows, be, Wd taps, bd, then the Wp rows of
+// this output-channel slice (each 32 channels = 8 float4 wide, the We rows cin wide).
+// goff: packed-weight offset at chunk 0; meta: LDS offset | channel within the chunk << 16
+// | 1 << 24 for the We rows (which advance 32 rows per chunk; the rest 32 channels).
+template <int K>
+__device__ __forceinline__ void weight_slot(const IrArgs& a, int j, int idx, int& goff,
+                                            int& meta) {
+    if (a.expand) {
+        const int cin4 = a.cin >> 2;
+        const int nwe = CC * cin4;
+        if (idx < nwe) {  // the chunk's We rows are one contiguous span
+            const int r = udiv(idx, a.m_cin4), q = idx - r * cin4;
+            goff = a.w_we + 4 * idx;
+            meta = (a.o_w + r * a.wsx + 4 * q) | (r << 16) | (1 << 24);
+            return;
+        }
+        idx -= nwe;
+        if (idx < 8) {
+            goff = a.w_be + 4 * idx;
+            meta = (a.o_be + 4 * idx) | ((4 * idx) << 16);
+            return;
+        }
+        idx -= 8;
+    }
+    if (idx < 8 * K * K) {
+        const int t = idx >> 3, q = idx & 7;
+        goff = a.w_wd + t * a.ce + 4 * q;
+        meta = (a.o_wd + t * CC + 4 * q) | ((4 * q) << 16);
+        return;
+    }
+    idx -= 8 * K * K;
+    if (idx < 8) {
+        goff = a.w_bd + 4 * idx;
+        meta = (a.o_bd + 4 * idx) | ((4 * idx) << 16);
+        return;
+    }
+    idx -= 8;
+    const int r = idx >> 3, q = idx & 7;
+    goff = a.w_wp + (j * a.coj + r) * a.ce + 4 * q;
+    meta = (a.o_wp + r * WPS + 4 * q) | ((4 * q) << 16);
+}
+
+// Loads (fetch) and LDS stores (put) of this thread's float4s of one chunk's weights,
+// unrolled by recursion so the staging registers stay registers.  Channels past ce (the
+// second half of a 16-channel last chunk) read as zeros.
+template <int U>
+__device__ __forceinline__ void fetch_weights(f4v (&pf)[NPF], const IrArgs& a,
+                                              const int (&goff)[NPF], const int (&meta)[NPF],
+                                              int tid, int nf, int ch) {
+    if constexpr (U < NPF) {
+        pf[U] = f4v{0.f, 0.f, 0.f, 0.f};
+        if (tid + 256 * U < nf && ch * CC + ((meta[U] >> 16) & 255) < a.ce) {
+            const int stp = (meta[U] >> 24) ? CC * a.cin : CC;
+            pf[U] = *reinterpret_cast<const f4v*>(a.w + goff[U] + stp * ch);
+        }
+        fetch_weights<U + 1>(pf, a, goff, meta, tid, nf, ch);
+    }
+}
+template <int U>
+__device__ __forceinline__ void put_weights(const f4v (&pf)[NPF], float* lds,
+                                            const int (&meta)[NPF], int tid, int nf) {
+    if constexpr (U < NPF) {
+        if (tid + 256 * U < nf) *reinterpret_cast<f4v*>(lds + (meta[U] & 0xFFFF)) = pf[U];
+        put_weights<U + 1>(pf, lds, meta, tid, nf);
+    }
+}
+
+// The expand and depthwise activations: none, ReLU or ReLU6 as one clamp (the host refuses
+// the others), so the per-element code has no branches.
+struct ActClamp {
+    float lo, hi;
+    bool on;
+    __device__ explicit ActClamp(int act)
+        : lo(0.f), hi(act == SHP_ACT_RELU6 ? 6.f : __builtin_huge_valf()), on(act != SHP_ACT_NONE) {}
+    __device__ float operator()(float v) const { return on ? fminf(fmaxf(v, lo), hi) : v; }
+};
+
+__device__ __forceinline__ floatx4 mfma4(f4v a, f4v b, floatx4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+}
+
+// K, ST: depthwise kernel size and stride; NBW: projection blocks (16 pixels x 16 output
+// channels) per wavefront, at most.
+template <int K, int ST, int NBW>
+__global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, li = lane & 15;
+    int id = blockIdx.x;
+    const int si = id % a.S;
+    id /= a.S;
+    const int j = id % a.J;
+    const int tile = id / a.J;  // (img, ty, tx) row-major
+    const int tx = tile % a.tiles_x;
+    const int ty = (tile / a.tiles_x) % a.tiles_y;
+    const int img = tile / (a.tiles_x * a.tiles_y);
+    const int oy0 = ty * a.th, ox0 = tx * a.tw;
+    const int iy0 = oy0 * ST - a.pt, ix0 = ox0 * ST - a.pl;
+    const int c_begin = si * a.cpw;
+    const int c_end = min(a.nchunk, c_begin + a.cpw);
+    const int cv = min(a.coj, a.cout - j * a.coj);  // output channels of this slice
+    const int nf = (a.expand ? CC * (a.cin >> 2) + 8 : 0) + 8 * K * K + 8 + 8 * cv;
+    const int P = a.th * a.tw;
+    const int nblk = a.pb * a.ob;
+    const int hrows = a.hpb * 16;
+
+    float* Xs = lds + a.o_x;
+    float* Ws = lds + a.o_w;
+    const float* Bes = lds + a.o_be;
+    const float* Wds = lds + a.o_wd;
+    const float* Bds = lds + a.o_bd;
+    float* Es = lds + a.o_e;
+    float* Ds = lds + a.o_d;
+    float* Wps = lds + a.o_wp;
+    int* hvalid = reinterpret_cast<int*>(lds + a.o_hv);  // halo row inside the image
+
+    // this thread's share of every chunk's weights, and the first chunk's loads
+    int goff[NPF], meta[NPF];
+#pragma unroll
+    for (int u = 0; u < NPF; ++u) {
+        goff[u] = meta[u] = 0;
+        if (tid + 256 * u < nf) weight_slot<K>(a, j, tid + 256 * u, goff[u], meta[u]);
+    }
+    f4v pf[NPF];  // (native vectors: HIP's float4 struct copies would pin them to scratch)
+    fetch_weights<0>(pf, a, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
+
+    // halo patch of x: hrows rows (halo pixels, row-major) of cin16 floats; zero outside
+    // the image, in the padding columns and in the rows past the patch (8 loads in flight
+    // per thread)
+    {
+        const int c4n = a.cin16 >> 2;
+        const int total = hrows * c4n;
+        for (int e0 = tid; e0 < total; e0 += 2048) {
+            f4v v[8];
+            int dst[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int e = e0 + 256 * t;
+                v[t] = f4v{0.f, 0.f, 0.f, 0.f};
+                dst[t] = -1;
+                if (e < total) {
+                    const int r = udiv(e, a.m_c4n), q = e - r * c4n;
+                    dst[t] = r * a.xs + 4 * q;
+                    if (r < a.hp && 4 * q < a.cin) {
+                        const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+                        const int iy = iy0 + hy, ix = ix0 + hx;
+                        if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_)
+                            v[t] = *reinterpret_cast<const f4v*>(
+                                a.x + (((int64_t)img * a.h + iy) * a.w_ + ix) * a.cin + 4 * q);
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                if (dst[t] >= 0) *reinterpret_cast<f4v*>(Xs + dst[t]) = v[t];
+        }
+    }
+    for (int r = tid; r < hrows; r += 256) {
+        const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+        const int iy = iy0 + hy, ix = ix0 + hx;
+        hvalid[r] = r < a.hp && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_;
+    }
+    // never written by the chunk staging: We padding columns, Wp rows past this slice and
+    // the depthwise rows past the tile's pixels (read by the projection as zeros)
+    if (a.expand && a.cin16 > a.cin) {
+        const int pc = a.cin16 - a.cin;
+        for (int e = tid; e < CC * pc; e += 256) Ws[(e / pc) * a.wsx + a.cin + e % pc] = 0.f;
+    }
+    for (int e = tid; e < (a.ob * 16 - cv) * CC; e += 256)
+        Wps[(cv + e / CC) * WPS + e % CC] = 0.f;
+    for (int e = tid; e < (a.pb * 16 - P) * CC; e += 256) Ds[(P + e / CC) * DS + e % CC] = 0.f;
+
+    floatx4 acc[NBW];
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int dc = tid & 31, dy = tid >> 5;  // depthwise: channel and output row of the tile
+    for (int ch = c_begin; ch < c_end; ++ch) {
+        __syncthreads();  // the previous chunk's readers are done with its weights, E and D
+        put_weights<0>(pf, lds, meta, tid, nf);
+        if (ch + 1 < c_end)  // the next chunk's weights load while this one computes
+            fetch_weights<0>(pf, a, goff, meta, tid, nf, ch + 1);
+        __syncthreads();
+        const int c0 = ch * CC;
+        const bool half = c0 + 16 >= a.ce;  // a 16-channel last chunk: one column block
+        if (a.expand) {
+            // E[halo pixel][32 channels]: lane group g sums the K quarter [g*Q, g*Q + Q) of
+            // cin16, so each lane reads 16 contiguous bytes of its row per 4 MFMA steps; the
+            // row block's x reads serve both column blocks, and the next step's operands are
+            // read before this step's products issue
+            const int Q = a.cin16 >> 2;
+            const ActClamp act_e(a.act_e);
+            const float be0 = Bes[li], be1 = Bes[16 + li];
+            const float* wb0 = Ws + li * a.wsx + g * Q;
+            const float* wb1 = wb0 + 16 * a.wsx;
+            for (int hb = wave; hb < a.hpb; hb += 8) {  // row blocks hb and hb + 4
+                const bool two = hb + 4 < a.hpb;
+                const float* xa0 = Xs + (hb * 16 + li) * a.xs + g * Q;
+                const float* xa1 = two ? xa0 + 64 * a.xs : xa0;
+                floatx4 e00 = {0.f, 0.f, 0.f, 0.f}, e01 = e00, e10 = e00, e11 = e00;
+                f4v x0 = *reinterpret_cast<const f4v*>(xa0);
+                f4v x1 = *reinterpret_cast<const f4v*>(xa1);
+                f4v b0 = *reinterpret_cast<const f4v*>(wb0);
+                f4v b1 = *reinterpret_cast<const f4v*>(wb1);
+                for (int u = 4; u <= Q; u += 4) {
+                    f4v nx0 = x0, nx1 = x1, nb0 = b0, nb1 = b1;
+                    if (u < Q) {
+                        nx0 = *reinterpret_cast<const f4v*>(xa0 + u);
+                        nx1 = *reinterpret_cast<const f4v*>(xa1 + u);
+                        nb0 = *reinterpret_cast<const f4v*>(wb0 + u);
+                        nb1 = *reinterpret_cast<const f4v*>(wb1 + u);
+                    }
+                    // zero weights past ce (a 16-channel last chunk) in the second column block
+                    e00 = mfma4(x0, b0, e00);
+                    e01 = mfma4(x0, b1, e01);
+                    if (two) {
+                        e10 = mfma4(x1, b0, e10);
+                        e11 = mfma4(x1, b1, e11);
+                    }
+                    x0 = nx0;
+                    x1 = nx1;
+                    b0 = nb0;
+                    b1 = nb1;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {  // accumulator r: row 4g + r, column li
+                    const int row = hb * 16 + 4 * g + r;
+                    const bool in = hvalid[row];
+                    Es[row * ES + li] = in ? act_e(e00[r] + be0) : 0.f;
+                    Es[row * ES + 16 + li] = in && !half ? act_e(e01[r] + be1) : 0.f;
+                    if (two) {
+                        const bool in1 = hvalid[row + 64];
+                        Es[(row + 64) * ES + li] = in1 ? act_e(e10[r] + be0) : 0.f;
+                        Es[(row + 64) * ES + 16 + li] = in1 && !half ? act_e(e11[r] + be1) : 0.f;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (dy < a.th) {
+            // depthwise, one output row of the tile per thread: the K x K window slides
+            // along the row in registers (ST new columns per pixel); taps bias first, then
+            // row by row as the reference sums them
+            const float* src = a.expand ? Es + dc : Xs + c0 + dc;
+            const int rs = a.expand ? ES : a.xs;
+            const ActClamp act_d(a.act_d);
+            float wk[K * K];
+#pragma unroll
+            for (int t = 0; t < K * K; ++t) wk[t] = Wds[t * CC + dc];
+            const float bd = Bds[dc];
+            float win[K][K];
+            const int r0 = dy * ST * a.hw;
+#pragma unroll
+            for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+                for (int kx = 0; kx < K; ++kx) win[ky][kx] = src[(r0 + ky * a.hw + kx) * rs];
+#pragma unroll
+            for (int px = 0; px < 8; ++px) {  // tw <= 8
+                if (px >= a.tw) break;
+                if (px > 0) {
+                    const int c1 = px * ST;
+#pragma unroll
+                    for (int ky = 0; ky < K; ++ky) {
+#pragma unroll
+                        for (int kx = 0; kx < K - ST; ++kx) win[ky][kx] = win[ky][kx + ST];
+#pragma unroll
+                        for (int kx = K - ST; kx < K; ++kx)
+                            win[ky][kx] = src[(r0 + ky * a.hw + c1 + kx) * rs];
+                    }
+                }
+                float sacc = bd;
+#pragma unroll
+                for (int ky = 0; ky < K; ++ky)
+#pragma unroll
+                    for (int kx = 0; kx < K; ++kx) sacc = fmaf(win[ky][kx], wk[ky * K + kx], sacc);
+                Ds[(dy * a.tw + px) * DS + dc] = act_d(sacc);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NBW; ++i) {  // project the chunk's 32 channels
+            const int b = wave + 4 * i;
+            if (b < nblk) {
+                const int pbi = b / a.ob, obi = b - pbi * a.ob;
+                const float* da = Ds + (pbi * 16 + li) * DS + 8 * g;
+                const float* wp = Wps + (obi * 16 + li) * WPS + 8 * g;
+                acc[i] = mfma4(*reinterpret_cast<const f4v*>(da), *reinterpret_cast<const f4v*>(wp),
+                               acc[i]);
+                acc[i] = mfma4(*reinterpret_cast<const f4v*>(da + 4),
+                               *reinterpret_cast<const f4v*>(wp + 4), acc[i]);
+            }
+        }
+    }
+
+    auto store = [&](int b, int l, floatx4 v) {  // bias, residual, activation of 4 outputs
+        const int pbi = b / a.ob, obi = b - pbi * a.ob;
+        const int oo = obi * 16 + (l & 15);
+        if (oo >= cv) return;
+        const int o = j * a.coj + oo;
+        const float bias = a.w[a.w_bp + o];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = pbi * 16 + 4 * (l >> 4) + r;
+            if (p >= P) continue;
+            const int py = udiv(p, a.m_tw), px = p - py * a.tw;
+            const int oy = oy0 + py, ox = ox0 + px;
+            if (oy >= a.oh || ox >= a.ow) continue;
+            const int64_t idx = (((int64_t)img * a.oh + oy) * a.ow + ox) * a.cout + o;
+            float vv = v[r] + bias;
+            if (a.res) vv += a.res[idx];
+            a.y[idx] = shpd::apply_act(vv, a.act_o, a.alpha);
+        }
+    };
+
+    if (a.S == 1) {
+#pragma unroll
+        for (int i = 0; i < NBW; ++i)
+            if (wave + 4 * i < nblk) store(wave + 4 * i, lane, acc[i]);
+        return;
+    }
+    // split expanded channels: partials, then the last arrival sums them
+    const int slot = tile * a.J + j;
+    const int W = nblk * 64;  // float4 positions of one split's partial (block, lane)
+    const __amdgpu_buffer_rsrc_t prs =
+        buffer_rsrc(a.partial + (int64_t)slot * a.S * W * 4, (int64_t)a.S * W * 4);
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+        const int b = wave + 4 * i;
+        if (b < nblk)
+            st_coh16(prs, (unsigned)((si * W + b * 64 + lane) * 16),
+                     make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]));
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are stored
+    __syncthreads();
+    int* flag = reinterpret_cast<int*>(lds + a.o_flag);
+    int* cnt = a.counters + slot;
+    if (tid == 0)
+        *flag = __hip_atomic_fetch_add((SHP_GLOBAL int*)cnt, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == a.S - 1;
+    __syncthreads();
+    if (!*flag) return;
+    // the last arrival: every thread sums up to 2 positions over the splits, in split order,
+    // with 8 splits x 2 positions of loads in flight, and stores their outputs
+    for (int f0 = tid; f0 < W; f0 += 512) {
+        f4v t[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) t[m] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < a.S; s0 += 8) {
+            float4 q[2][8];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (f0 + 256 * m < W && s0 + u < a.S)
+                        q[m][u] = ld_coh16(prs, (unsigned)(((s0 + u) * W + f0 + 256 * m) * 16), 0);
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (f0 + 256 * m < W && s0 + u < a.S)
+                        t[m] += f4v{q[m][u].x, q[m][u].y, q[m][u].z, q[m][u].w};
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const int f = f0 + 256 * m;
+            if (f < W) store(f >> 6, f & 63, floatx4{t[m].x, t[m].y, t[m].z, t[m].w});
+        }
+    }
+    if (tid == 0)
+        __hip_atomic_store((SHP_GLOBAL int*)cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- host: shape, plan, launch ------------------------------------------------------------
+
+struct IrShape {
+    int n, cin, h, w, ce, cout, oh, ow, k, s, pt, pl, expand, act_e, act_d;
+};
+
+struct IrPlan {
+    int th = 0, tw = 0, S = 1, J = 1;
+    double cost = 1e30;
+};
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// LDS row stride for rows of c16 floats: congruent to 4 modulo 32, so the 16 rows one
+// 16-byte MFMA operand read touches start 4 banks apart
+int row_stride(int c16) { return c16 + (36 - c16 % 32) % 32; }
+
+// Derived sizes of one plan (everything the kernel arguments need except pointers).
+struct IrGeom {
+    int tiles_y, tiles_x, tiles, hh, hw, hp, hpb, cin16, xs, wsx, nchunk, cpw, S, J, coj, ob, pb;
+    int nblk, nbw, nf_max, lds_floats;
+    int o_x, o_w, o_be, o_wd, o_bd, o_e, o_d, o_wp, o_hv, o_flag;
+};
+
+IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
+    IrGeom g{};
+    g.tiles_y = ceil_div(sh.oh, th);
+    g.tiles_x = ceil_div(sh.ow, tw);
+    g.tiles = sh.n * g.tiles_y * g.tiles_x;
+    g.hh = (th - 1) * sh.s + sh.k;
+    g.hw = (tw - 1) * sh.s + sh.k;
+    g.hp = g.hh * g.hw;
+    g.hpb = ceil_div(g.hp, 16);
+    g.cin16 = ceil_div(sh.cin, 16) * 16;
+    g.xs = row_stride(g.cin16);
+    g.wsx = g.xs;
+    g.nchunk = ceil_div(sh.ce, CC);
+    g.cpw = ceil_div(g.nchunk, std::max(1, std::min(S, g.nchunk)));
+    g.S = ceil_div(g.nchunk, g.cpw);  // no empty split
+    const int ob_all = ceil_div(sh.cout, 16);
+    g.ob = ceil_div(ob_all, std::max(1, std::min(J, ob_all)));
+    g.coj = 16 * g.ob;
+    g.J = ceil_div(sh.cout, g.coj);
+    g.pb = ceil_div(th * tw, 16);
+    g.nblk = g.pb * g.ob;
+    g.nbw = ceil_div(g.nblk, 4);
+    g.nf_max = (sh.expand ? CC * (sh.cin / 4) + 8 : 0) + 8 * sh.k * sh.k + 8 + 8 * g.coj;
+    int o = 0;
+    g.o_x = o;   o += g.hpb * 16 * g.xs;
+    g.o_w = o;   o += sh.expand ? CC * g.wsx : 0;
+    g.o_be = o;  o += CC;
+    g.o_wd = o;  o += sh.k * sh.k * CC;
+    g.o_bd = o;  o += CC;
+    g.o_e = o;   o += sh.expand ? g.hpb * 16 * ES : 0;
+    g.o_d = o;   o += g.pb * 16 * DS;
+    g.o_wp = o;  o += g.ob * 16 * WPS;
+    g.o_hv = o;  o += g.hpb * 16;
+    g.o_flag = o; o += 4;
+    g.lds_floats = o;
+    return g;
+}
+
+bool geometry_ok(const IrGeom& g) {
+    return g.lds_floats * 4 <= kMaxLds && g.nbw <= 20 && g.nf_max <= 256 * NPF &&
+           (int64_t)g.S * g.nblk * 1024 < (1ll << 31) &&
+           (g.S == 1 || (int64_t)g.tiles * g.J <= (int64_t)(shp::kSplitCounterBytes / sizeof(int))) &&
+           (int64_t)g.tiles * g.J * g.S < (1ll << 31);
+}
+
+size_t workspace_bytes(const IrGeom& g) {
+    if (g.S <= 1) return 0;
+    return shp::kSplitCounterBytes + (size_t)g.tiles * g.J * g.S * g.nblk * 256 * sizeof(float);
+}
+
+// Estimated time of a plan in CU cycles (constants from MI355X phase timings of the
+// kernel): the workgroups run in rounds of 256 (or 512 where two fit in a CU, each then
+// ~1.6x slower); a workgroup pays the halo load, per 32-channel chunk the expand MFMAs of
+// its busiest wavefront, the depthwise window loads and taps, the projection MFMAs and the
+// chunk's barriers and weight staging, and with split channels the partial stores, the
+// arrival count and, for the last arrival, the split-ordered sum in rounds of loads.
+double plan_cost(const IrShape& sh, const IrGeom& g) {
+    const double expand = sh.expand ? ceil_div(g.hpb, 4) * g.cin16 * 16.0 : 0.0;
+    const double dw = g.hw * sh.k * 24.0 + (ceil_div(g.hp, g.hw) / sh.s) * 0.0 +
+                      (g.hw / sh.s) * sh.k * sh.k * 4.0;
+    const double proj = g.nbw * 8.0 * 32.0;
+    const double chunk = expand + dw + proj + 1500.0;
+    double wg = 7000.0 + g.cpw * chunk + 1000.0;
+    if (g.S > 1)
+        wg += 5000.0 + ceil_div(g.S, 8) * ceil_div(g.nblk * 64, 512) * 4000.0 + 2000.0;
+    const int occ = std::max(1, std::min(2, kMaxLds / std::max(1, g.lds_floats * 4)));
+    const double wgs = (double)g.tiles * g.J * g.S;
+    const double rounds = std::ceil(wgs / (256.0 * occ));
+    return rounds * wg * (occ > 1 && wgs > 256.0 ? 1.6 : 1.0);
+}
+
+// Plans measured best on MI355X for the MBConv blocks of the benchmark configs (every tile,
+// split and output-channel slice per block, each timed as 20 launches replayed from a
+// hipGraph), and whether one launch beat the three operators (conv2d_nhwc,
+// depthwise_conv2d_nhwc, conv2d_nhwc) in the whole model's graph replay.  The cost model and
+// the rule of fusion_pays cover every other shape.
+struct TunedBlock {
+    int n, cin, h, w, ce, cout, k, s, expand;
+    int th, tw, S, J;
+    bool fuse;
+};
+const TunedBlock kTunedBlocks[] = {
+    // MobileNetV2-1.0 batch 1 (us in the model's graph replay: one launch / three launches)
+    {1, 32, 112, 112, 32, 16, 3, 1, 0, 7, 7, 1, 1, true},     // block0: 10.2 / 10.4
+    {1, 16, 112, 112, 96, 24, 3, 2, 1, 8, 2, 1, 1, true},     // block1: 16.3 / 18.3
+    {1, 24, 56, 56, 144, 24, 3, 1, 1, 8, 4, 4, 1, true},      // block2: 15.9 / 23.5
+    {1, 24, 56, 56, 144, 32, 3, 2, 1, 8, 2, 3, 1, true},      // block3: 16.4 / 20.1
+    {1, 32, 28, 28, 192, 32, 3, 1, 1, 8, 4, 6, 1, true},      // block4-5: 12.3 / 21.6-27.4
+    {1, 32, 28, 28, 192, 64, 3, 2, 1, 4, 2, 6, 1, true},      // block6: 12.3 / 20.0
+    {1, 64, 14, 14, 384, 64, 3, 1, 1, 8, 2, 12, 2, true},     // block7-9: 14.4-15.0 / 21.3-23.2
+    {1, 64, 14, 14, 384, 96, 3, 1, 1, 8, 2, 12, 2, true},     // block10: 14.2 / 21.2
+    {1, 96, 14, 14, 576, 96, 3, 1, 1, 7, 2, 16, 2, true},     // block11-12: 17.5 / 22.4-23.0
+    {1, 96, 14, 14, 576, 160, 3, 2, 1, 7, 1, 12, 4, true},    // block13: 17.7 / 23.0
+    {1, 160, 7, 7, 960, 160, 3, 1, 1, 7, 2, 16, 3, true},     // block14-15: 21.1 / 24.6
+    {1, 160, 7, 7, 960, 320, 3, 1, 1, 7, 2, 16, 4, true},     // block16: 23.2 / 25.4
+    // EfficientNet-Lite0 batch 8
+    {8, 32, 112, 112, 32, 16, 3, 1, 0, 8, 7, 1, 1, false},    // block0: 32.0 / 25.1
+    {8, 16, 112, 112, 96, 24, 3, 2, 1, 7, 4, 1, 1, true},     // block1: 39.3 / 43.4
+    {8, 24, 56, 56, 144, 24, 3, 1, 1, 7, 7, 1, 1, true},      // block2: 30.0 / 41.2
+    {8, 24, 56, 56, 144, 40, 5, 2, 1, 7, 2, 1, 1, true},      // block3: 30.3 / 36.7
+    {8, 40, 28, 28, 240, 40, 5, 1, 1, 7, 7, 2, 1, true},      // block4: 32.6 / 38.4
+    {8, 40, 28, 28, 240, 80, 3, 2, 1, 7, 2, 4, 1, false},     // block5: 32.4 / 29.3
+    {8, 80, 14, 14, 480, 80, 3, 1, 1, 8, 4, 8, 1, false},     // block6-7: 26.8-28.1 / 24.9-25.1
+    {8, 80, 14, 14, 480, 112, 5, 1, 1, 4, 4, 4, 1, false},    // block8: 32.0 / 30.2
+    {8, 112, 14, 14, 672, 112, 5, 1, 1, 4, 4, 4, 1, false},   // block9-10: 44.3 / 35.7 (alone)
+    {8, 112, 14, 14, 672, 192, 5, 2, 1, 7, 2, 8, 1, false},   // block11: 33.4 / 29.0 (alone)
+    {8, 192, 7, 7, 1152, 192, 5, 1, 1, 7, 4, 8, 2, false},    // block12-14: 53.6 / 29.8 (alone)
+    {8, 192, 7, 7, 1152, 320, 3, 1, 1, 7, 4, 8, 2, false},    // block15: 57.2 / 27.7 (alone)
+};
+
+const TunedBlock* tuned_block(const IrShape& sh) {
+    for (const TunedBlock& t : kTunedBlocks)
+        if (t.n == sh.n && t.cin == sh.cin && t.h == sh.h && t.w == sh.w && t.ce == sh.ce &&
+            t.cout == sh.cout && t.k == sh.k && t.s == sh.s && t.expand == sh.expand)
+            return &t;
+    return nullptr;
+}
+
+// Whether one launch is expected to beat the three-operator form: the measured verdict for
+// the blocks above; elsewhere, for blocks with an expand, where the separate launches are
+// latency-bound (at most 1024 output pixels in the batch) or the expand is a thin,
+// memory-bound product (cin <= 48) whose output the fused form never writes.
+bool fusion_pays(const IrShape& sh) {
+    if (const TunedBlock* t = tuned_block(sh)) return t->fuse;
+    return sh.expand && ((int64_t)sh.n * sh.oh * sh.ow <= 1024 || sh.cin <= 48);
+}
+
+IrPlan choose_plan(const IrShape& sh, const shp::GemmTune& tn, bool allow_split) {
+    static std::mutex mu;
+    static std::map<std::tuple<std::vector<int>, bool>, IrPlan> cache;
+    const std::vector<int> key{sh.n, sh.cin, sh.h, sh.w, sh.ce, sh.cout, sh.oh, sh.ow, sh.k,
+                               sh.s, sh.pt, sh.pl, sh.expand, tn.ir_th, tn.ir_tw, tn.ir_s,
+                               tn.ir_j};
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find({key, allow_split});
+        if (it != cache.end()) return it->second;
+    }
+    IrPlan best;
+    const TunedBlock* tb = tuned_block(sh);
+    if (tb && !tn.ir_th && !tn.ir_tw && !tn.ir_s && !tn.ir_j && (tb->S == 1 || allow_split)) {
+        const IrGeom g = geometry(sh, tb->th, tb->tw, tb->S, tb->J);
+        if (geometry_ok(g)) best = IrPlan{tb->th, tb->tw, g.S, g.J, plan_cost(sh, g)};
+    }
+    const int nchunk = ceil_div(sh.ce, CC);
+    const int ob_all = ceil_div(sh.cout, 16);
+    const int force_s = std::min(tn.ir_s, nchunk), force_j = std::min(tn.ir_j, ob_all);
+    static const int kEdge[] = {8, 7, 4, 2, 1};
+    if (best.th) {
+        std::lock_guard<std::mutex> lk(mu);
+        cache[{key, allow_split}] = best;
+        return best;
+    }
+    static const int kSplit[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 15, 16, 20, 24, 30, 36, 40, 48, 60, 72};
+    for (int th0 : kEdge) {
+        const int th = std::min(th0, sh.oh);
+        if (tn.ir_th && th != std::min(tn.ir_th, sh.oh)) continue;
+        for (int tw0 : kEdge) {
+            const int tw = std::min(tw0, sh.ow);
+            if (tn.ir_tw && tw != std::min(tn.ir_tw, sh.ow)) continue;
+            if (th * tw > 64) continue;
+            std::vector<int> splits(std::begin(kSplit), std::end(kSplit));
+            if (force_s > 0) splits.assign(1, force_s);
+            for (int S : splits) {
+                if (S > nchunk || (S > 1 && !allow_split)) continue;
+                for (int J = 1; J <= ob_all && J <= 8; ++J) {
+                    if (force_j > 0 && J != force_j) continue;
+                    const IrGeom g = geometry(sh, th, tw, S, J);
+                    if (g.S != S && force_s <= 0) continue;  // duplicate of a smaller S
+                    if (g.J != J && force_j <= 0) continue;
+                    if (!geometry_ok(g)) continue;
+                    const double c = plan_cost(sh, g);
+                    if (c < best.cost * 0.999) best = IrPlan{th, tw, g.S, g.J, c};
+                }
+            }
+        }
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    cache[{key, allow_split}] = best;
+    return best;
+}
+
+int parse(const int32_t* q, size_t n, IrShape& sh) {
+    if (n < 16)
+        return shp::fail(SHP_ERR_PUSH, "inverted_residual_nhwc needs 16 push constants");
+    sh = IrShape{q[0], q[1], q[2], q[3], q[4], q[5], q[6], q[7], q[8], q[9], q[10], q[11],
+                 q[12], q[13], q[14]};
+    if (sh.n <= 0 || sh.cin <= 0 || sh.h <= 0 || sh.w <= 0 || sh.ce <= 0 || sh.cout <= 0 ||
+        sh.oh <= 0 || sh.ow <= 0 || sh.k <= 0 || sh.s <= 0)
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: non-positive dim");
+    if ((sh.k != 3 && sh.k != 5) || sh.s > 2 || sh.pt < 0 || sh.pl < 0 || sh.pt >= sh.k ||
+        sh.pl >= sh.k)
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "inverted_residual_nhwc: kernel 3 or 5, stride 1 or 2, padding < kernel");
+    if (sh.cin % 4 || sh.ce % 16)
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "inverted_residual_nhwc: cin must be a multiple of 4, ce of 16");
+    auto clamp_act = [](int act) {
+        return act == SHP_ACT_NONE || act == SHP_ACT_RELU || act == SHP_ACT_RELU6;
+    };
+    if (!clamp_act(sh.act_e) || !clamp_act(sh.act_d))
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "inverted_residual_nhwc: expand/depthwise activation must be none, "
+                         "relu or relu6");
+    if (sh.expand != 0 && sh.expand != 1)
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: expand must be 0 or 1");
+    if (!sh.expand && sh.ce != sh.cin)
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: ce != cin without expand");
+    if ((int64_t)(sh.oh - 1) * sh.s - sh.pt >= sh.h || (int64_t)(sh.ow - 1) * sh.s - sh.pl >= sh.w)
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: output window outside input");
+    if ((int64_t)q[15] != (int64_t)sh.n * sh.oh * sh.ow * sh.cout)
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: total != n*oh*ow*cout");
+    const int64_t wn = (sh.expand ? (int64_t)sh.ce * sh.cin + sh.ce : 0) +
+                       (int64_t)sh.k * sh.k * sh.ce + sh.ce + (int64_t)sh.cout * sh.ce + sh.cout;
+    if (wn >= (1ll << 31) || (int64_t)sh.n * sh.h * sh.w * sh.cin >= (1ll << 40))
+        return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: tensors too large");
+    return SHP_OK;
+}
+
+template <int K, int ST, int NBW>
+int launch_variant(hipStream_t stream, const IrArgs& a, unsigned grid, size_t lds) {
+    if (lds > 64 * 1024)
+        SHP_HIP_CHECK(hipFuncSetAttribute((const void*)ir_kernel<K, ST, NBW>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((ir_kernel<K, ST, NBW>), dim3(grid), dim3(256), lds, stream, a);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
+template <int K, int ST>
+int launch_nbw(hipStream_t stream, const IrArgs& a, int nbw, unsigned grid, size_t lds) {
+    if (nbw <= 2) return launch_variant<K, ST, 2>(stream, a, grid, lds);
+    if (nbw <= 4) return launch_variant<K, ST, 4>(stream, a, grid, lds);
+    if (nbw <= 8) return launch_variant<K, ST, 8>(stream, a, grid, lds);
+    return launch_variant<K, ST, 20>(stream, a, grid, lds);
+}
+
+int launch_ir(const shp::Launch& l) {
+    IrShape sh;
+    int rc = parse(l.push, l.n_push, sh);
+    if (rc) return rc;
+    rc = shp::check_total(l, (int64_t)sh.n * sh.oh * sh.ow * sh.cout, "inverted_residual_nhwc");
+    if (rc) return rc;
+    if (l.epi->bias)
+        return shp::fail(SHP_ERR_INVALID,
+                         "inverted_residual_nhwc: the biases are part of the packed weights");
+    auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!l.in0 || !l.in1 || !l.out || !a16(l.in0) || !a16(l.in1))
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "inverted_residual_nhwc: x and the weights must be 16-byte aligned");
+    static const shp::GemmTune kAuto;
+    const shp::GemmTune& tn = l.tune ? *l.tune : kAuto;
+    IrPlan pl = choose_plan(sh, tn, true);
+    IrGeom g = pl.th ? geometry(sh, pl.th, pl.tw, pl.S, pl.J) : IrGeom{};
+    if (pl.th && g.S > 1 && (l.workspace == nullptr || l.workspace_bytes < workspace_bytes(g))) {
+        pl = choose_plan(sh, tn, false);  // no room for partials: one split per tile
+        if (pl.th) g = geometry(sh, pl.th, pl.tw, pl.S, pl.J);
+    }
+    if (!pl.th)
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "inverted_residual_nhwc: no tile of this block fits the LDS");
+    IrArgs a{};
+    a.x = (const float*)l.in0;
+    a.w = (const float*)l.in1;
+    a.y = (float*)l.out;
+    a.res = l.epi->residual;
+    a.partial = g.S > 1 ? l.workspace + shp::kSplitCounterBytes / sizeof(float) : nullptr;
+    a.counters = g.S > 1 ? reinterpret_cast<int*>(l.workspace) : nullptr;
+    a.n = sh.n; a.h = sh.h; a.w_ = sh.w; a.cin = sh.cin; a.ce = sh.ce; a.cout = sh.cout;
+    a.oh = sh.oh; a.ow = sh.ow; a.pt = sh.pt; a.pl = sh.pl;
+    a.expand = sh.expand; a.act_e = sh.act_e; a.act_d = sh.act_d; a.act_o = l.epi->act;
+    a.alpha = l.epi->alpha;
+    a.th = pl.th; a.tw = pl.tw; a.tiles_y = g.tiles_y; a.tiles_x = g.tiles_x;
+    a.hw = g.hw; a.hp = g.hp; a.hpb = g.hpb;
+    a.cin16 = g.cin16; a.xs = g.xs; a.wsx = g.wsx;
+    a.nchunk = g.nchunk; a.cpw = g.cpw; a.S = g.S;
+    a.J = g.J; a.coj = g.coj; a.ob = g.ob; a.pb = g.pb;
+    a.o_x = g.o_x; a.o_w = g.o_w; a.o_be = g.o_be; a.o_wd = g.o_wd; a.o_bd = g.o_bd;
+    a.o_e = g.o_e; a.o_d = g.o_d; a.o_wp = g.o_wp; a.o_hv = g.o_hv; a.o_flag = g.o_flag;
+    auto magic = [](int d) { return (unsigned)((0x100000000ull + (uint64_t)d - 1) / (uint64_t)d); };
+    a.m_cin4 = magic(sh.cin / 4);
+    a.m_c4n = magic(g.cin16 / 4);
+    a.m_hw = magic(g.hw);
+    a.m_tw = magic(pl.tw);
+    int o = 0;
+    if (sh.expand) {
+        a.w_we = 0;
+        a.w_be = sh.ce * sh.cin;
+        o = a.w_be + sh.ce;
+    }
+    a.w_wd = o;
+    a.w_bd = a.w_wd + sh.k * sh.k * sh.ce;
+    a.w_wp = a.w_bd + sh.ce;
+    a.w_bp = a.w_wp + sh.cout * sh.ce;
+    const unsigned grid = (unsigned)((int64_t)g.tiles * g.J * g.S);
+    const size_t lds = (size_t)g.lds_floats * sizeof(float);
+    if (sh.k == 3)
+        return sh.s == 1 ? launch_nbw<3, 1>(l.stream, a, g.nbw, grid, lds)
+                         : launch_nbw<3, 2>(l.stream, a, g.nbw, grid, lds);
+    return sh.s == 1 ? launch_nbw<5, 1>(l.stream, a, g.nbw, grid, lds)
+                     : launch_nbw<5, 2>(l.stream, a, g.nbw, grid, lds);
+}
+
+}  // namespace
+
+namespace shp {
+
+bool block_fusion_pays(const int32_t* push, size_t n_push) {
+    IrShape sh;
+    if (!push || parse(push, n_push, sh) != SHP_OK) {
+        set_error("");
+        return false;
+    }
+    static const GemmTune kAuto;
+    return fusion_pays(sh) && choose_plan(sh, kAuto, true).th > 0;
+}
+
+size_t block_workspace_for_kernel(const int32_t* push, size_t n_push, const GemmTune* tune) {
+    IrShape sh;
+    if (!push || parse(push, n_push, sh) != SHP_OK) {
+        set_error("");
+        return 0;
+    }
+    static const GemmTune kAuto;
+    const IrPlan pl = choose_plan(sh, tune ? *tune : kAuto, true);
+    if (!pl.th) return 0;
+    return workspace_bytes(geometry(sh, pl.th, pl.tw, pl.S, pl.J));
+}
+
+}  // namespace shp
+
+// The plan the launcher picks for this push vector (default tune, workspace large enough)
+// and whether one launch is expected to beat the three operators:
+// {th, tw, S, J, LDS bytes, workgroups, projection blocks per wavefront, fusion pays}.
+extern "C" int shp_block_plan(const int32_t* push, size_t n_push, int32_t* out8) {
+    IrShape sh;
+    if (!push || !out8) return shp::fail(SHP_ERR_INVALID, "shp_block_plan: null argument");
+    int rc = parse(push, n_push, sh);
+    if (rc) return rc;
+    static const shp::GemmTune kAuto;
+    const IrPlan pl = choose_plan(sh, kAuto, true);
+    if (!pl.th) return shp::fail(SHP_ERR_UNSUPPORTED, "shp_block_plan: no plan");
+    const IrGeom g = geometry(sh, pl.th, pl.tw, pl.S, pl.J);
+    const int32_t v[8] = {pl.th, pl.tw, g.S, g.J, g.lds_floats * 4, g.tiles * g.J * g.S, g.nbw,
+                          fusion_pays(sh) ? 1 : 0};
+    std::memcpy(out8, v, sizeof v);
+    return SHP_OK;
+}
+
+namespace shp {
+
+KernelEntry kBlockKernels[] = {
+    {"inverted_residual_nhwc", 16, true, launch_ir},
+};
+const int kBlockKernelCount = sizeof(kBlockKernels) / sizeof(kBlockKernels[0]);
+
+}  // namespace shp

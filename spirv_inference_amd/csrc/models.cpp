@@ -297,6 +297,44 @@ struct MBConv {
     int expand, k, s, c, n;
 };
 
+// The push vector of one MBConv block as a single inverted_residual_nhwc launch.
+std::vector<int32_t> block_push(const Act4& x, int expand, int k, int s, int cout) {
+    const int ce = expand != 1 ? x.c * expand : x.c;
+    int oh = (x.h + s - 1) / s, ow = (x.w + s - 1) / s;
+    int pt, pl;
+    same_padding(x.h, x.w, oh, ow, k, k, s, s, pt, pl);
+    return {x.n, x.c, x.h, x.w, ce, cout, oh, ow, k, s, pt, pl, expand != 1 ? 1 : 0,
+            SHP_ACT_RELU6, SHP_ACT_RELU6, (int32_t)((int64_t)x.n * oh * ow * cout)};
+}
+
+// One MBConv block as a single inverted_residual_nhwc launch: the three operators' weight
+// tensors packed back to back in one tensor and filled in the same order with the same
+// distributions (so the weights equal those of the three-operator graph of the same seed).
+Act4 tfl_block(Model& m, Act4 x, int expand, int k, int s, int cout, bool residual,
+               const char* label) {
+    const int ce = expand != 1 ? x.c * expand : x.c;
+    int oh = (x.h + s - 1) / s, ow = (x.w + s - 1) / s;
+    const uint64_t ne = expand != 1 ? (uint64_t)ce * x.c + ce : 0;
+    const uint64_t nd = (uint64_t)k * k * ce + ce, np = (uint64_t)cout * ce + cout;
+    int w = m.tensor(ne + nd + np, 1);
+    if (expand != 1) {
+        m.fill_normal(w, 0, (uint64_t)ce * x.c, std::sqrt(2.0f / (float)x.c));
+        m.fill_normal(w, (uint64_t)ce * x.c, ce, 0.01f);
+    }
+    m.fill_normal(w, ne, (uint64_t)k * k * ce, std::sqrt(2.0f / (float)(k * k)));
+    m.fill_normal(w, ne + (uint64_t)k * k * ce, ce, 0.01f);
+    m.fill_normal(w, ne + nd, (uint64_t)cout * ce, std::sqrt(2.0f / (float)ce));
+    m.fill_normal(w, ne + nd + (uint64_t)cout * ce, cout, 0.01f);
+    m.weight_bytes += (double)(ne + nd + np) * 4.0;
+    int y = m.tensor((uint64_t)x.n * oh * ow * cout);
+    const int64_t total = (int64_t)x.n * oh * ow * cout;
+    m.op("inverted_residual_nhwc", x.t, w, y, block_push(x, expand, k, s, cout), -1,
+         residual ? x.t : -1, SHP_ACT_NONE, 0.0f, label);
+    if (expand != 1) m.flops += 2.0 * (double)x.n * x.h * x.w * x.c * ce;
+    m.flops += 2.0 * (double)x.n * oh * ow * ce * k * k + 2.0 * (double)total * ce;
+    return Act4{y, x.n, oh, ow, cout};
+}
+
 int tfl_net(Model& m, int batch, const MBConv* cfg, int ncfg, int stem_c) {
     const int n = batch;
     int in = m.tensor((uint64_t)n * 224 * 224 * 3, 2);
@@ -312,6 +350,14 @@ int tfl_net(Model& m, int batch, const MBConv* cfg, int ncfg, int stem_c) {
     for (int i = 0; i < ncfg; ++i) {
         for (int r = 0; r < cfg[i].n; ++r, ++bi) {
             int s = r == 0 ? cfg[i].s : 1;
+            const int fuse = m.ctx->tune.ir_fuse;
+            const std::vector<int32_t> bp = block_push(x, cfg[i].expand, cfg[i].k, s, cfg[i].c);
+            if (fuse > 0 || (fuse == 0 && block_fusion_pays(bp.data(), bp.size()))) {
+                std::snprintf(label, sizeof label, "block%d_mbconv", bi);
+                x = tfl_block(m, x, cfg[i].expand, cfg[i].k, s, cfg[i].c,
+                              s == 1 && x.c == cfg[i].c, label);
+                continue;
+            }
             Act4 in_x = x;
             Act4 h = x;
             if (cfg[i].expand != 1) {

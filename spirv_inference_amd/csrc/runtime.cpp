@@ -45,6 +45,7 @@ std::vector<const KernelEntry*>& registry() {
         add(kSpatialKernels, kSpatialKernelCount);
         add(kDecodeKernels, kDecodeKernelCount);
         add(kHloOpKernels, kHloOpKernelCount);
+        add(kBlockKernels, kBlockKernelCount);
         return r;
     }();
     return reg;
@@ -338,6 +339,11 @@ int shp_tune(shp_ctx* ctx, const char* key, int value) {
     else if (k == "gemm_stem") t.stem = value;
     else if (k == "dw_tile") t.dw = value;
     else if (k == "gemm_group") t.group = value;
+    else if (k == "ir_th") t.ir_th = value;
+    else if (k == "ir_tw") t.ir_tw = value;
+    else if (k == "ir_splits") t.ir_s = value;
+    else if (k == "ir_cout_splits") t.ir_j = value;
+    else if (k == "ir_fuse") t.ir_fuse = value;
     else return fail(SHP_ERR_INVALID, "shp_tune: unknown key '" + k + "'");
     return SHP_OK;
 }

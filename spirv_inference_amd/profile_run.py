@@ -45,6 +45,10 @@ def op_work(op, elems) -> tuple[float, float]:
         flops = 4.0 * q[0] * q[1] * q[2] * q[2] * q[3]
     elif k in ("depthwise_conv2d", "depthwise_conv2d_nhwc"):
         flops = 2.0 * op.out_elems * q[6] * q[7]  # push {n, c, ih, iw, oh, ow, kh, kw, ...}
+    elif k == "inverted_residual_nhwc":  # {n, cin, h, w, ce, cout, oh, ow, k, s, .., expand}
+        px_in, px_out = q[0] * q[2] * q[3], q[0] * q[6] * q[7]
+        flops = 2.0 * (px_in * q[1] * q[4] * q[12] + px_out * q[4] * q[8] * q[8] +
+                       px_out * q[4] * q[5])
     nbytes = 4.0 * (sum(ins) + op.out_elems + extra)
     return flops, nbytes
 

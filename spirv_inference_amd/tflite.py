@@ -597,7 +597,11 @@ class TfliteExecutor:
     unary launch.  A CONV_2D without activation whose output is read only by an ADD of an
     equal-sized tensor computed earlier (a residual connection) runs as one conv2d_nhwc launch
     with that tensor as the epilogue's residual and the ADD's activation; the ADD then
-    dispatches nothing.  Anything else raises, like the reference's scheduler.
+    dispatches nothing.  An inverted-residual chain, [1x1 CONV_2D] -> DEPTHWISE_CONV_2D ->
+    1x1 CONV_2D [-> residual ADD], whose intermediates nothing else reads, runs as one
+    inverted_residual_nhwc launch at the projection where the library expects that to beat
+    the three launches (shp_block_plan); fuse_blocks=True fuses every chain the kernel takes,
+    False none.  Anything else raises, like the reference's scheduler.
 
     run(graph=True) replays the launch sequence from one hipGraph: the first such call runs
     eagerly if nothing ran yet (so every buffer, packed weight and split-K workspace exists),
@@ -605,7 +609,7 @@ class TfliteExecutor:
     buffers across runs, so set_input() between replays feeds the graph.
     """
 
-    def __init__(self, ctx, model: TfliteModel):
+    def __init__(self, ctx, model: TfliteModel, fuse_blocks: Optional[bool] = None):
         self.ctx, self.model = ctx, model
         self.order = topological_order(model)
         self.dev: Dict[int, object] = {}
@@ -623,6 +627,7 @@ class TfliteExecutor:
         self.op_log: List[dict] = []
         self._check_aliases()
         self.residual_adds = self._find_residual_adds()
+        self.blocks = self._find_blocks(fuse_blocks is None) if fuse_blocks is not False else {}
         self._graph = None
         self._warm = False
 
@@ -678,6 +683,125 @@ class TfliteExecutor:
                 continue  # the residual must exist when the convolution runs
             out[op.index] = (add.index, other)
         return out
+
+    def _find_blocks(self, only_if_faster: bool = True) -> Dict[int, dict]:
+        """{projection operator index: block} for every inverted-residual chain the fused
+        kernel takes (see the class docstring): 1x1 stride-1 convolutions with constant
+        weights, a depthwise with a square 3x3 or 5x5 kernel, stride 1 or 2, multiplier 1 and
+        no dilation, ReLU / ReLU6 / no activation before the projection, intermediates read
+        by the next operator only and not model outputs; the kernel's own plan query decides
+        the rest (channel multiples, and with only_if_faster whether one launch pays)."""
+        producer, readers = {}, {}
+        for op in self.model.operators:
+            for t in op.outputs:
+                producer[t] = op.index
+            for t in op.inputs:
+                readers.setdefault(t, []).append(op.index)
+        acts = ("none", "relu", "relu6")
+        ops = self.model.operators
+
+        def sole_reader(t):
+            r = readers.get(t, [])
+            return r[0] if len(r) == 1 and t not in self.model.outputs else None
+
+        def const_bias(op):
+            return len(op.inputs) < 3 or op.inputs[2] < 0 or op.inputs[2] in self.consts
+
+        def pointwise(op):
+            if op.builtin != "CONV_2D" or op.inputs[1] not in self.consts or not const_bias(op):
+                return False
+            o = decode_options(op)
+            _, kh, kw, _ = self._shape(op.inputs[1])
+            return (kh, kw, o["stride_h"], o["stride_w"], o["dilation_h_factor"],
+                    o["dilation_w_factor"]) == (1, 1, 1, 1, 1, 1) and o["fused_activation"] in acts
+
+        out = {}
+        for dw in ops:
+            if dw.builtin != "DEPTHWISE_CONV_2D" or dw.inputs[1] not in self.consts:
+                continue
+            o = decode_options(dw)
+            _, kh, kw, c = self._shape(dw.inputs[1])
+            if (o["depth_multiplier"] != 1 or kh != kw or kh not in (3, 5) or o["stride_h"] != o["stride_w"]
+                    or o["stride_h"] not in (1, 2) or not const_bias(dw)
+                    or (o["dilation_h_factor"], o["dilation_w_factor"]) != (1, 1)
+                    or o["fused_activation"] not in acts):
+                continue
+            pi = sole_reader(dw.outputs[0])
+            if pi is None or not pointwise(ops[pi]) or ops[pi].inputs[0] != dw.outputs[0]:
+                continue
+            src, ei = dw.inputs[0], producer.get(dw.inputs[0])
+            if ei is not None and pointwise(ops[ei]) and sole_reader(src) == dw.index:
+                src = ops[ei].inputs[0]
+            else:
+                ei = None
+            blk = {"expand": ei, "dw": dw.index, "src": src}
+            plan = self._block_plan(ops[pi], blk)
+            if plan is None or (only_if_faster and not plan[7]):
+                continue
+            out[pi] = blk
+        return out
+
+    def _block_push(self, proj: Operator, blk: dict) -> List[int]:
+        from ._lib import ACT
+        ops = self.model.operators
+        dw = ops[blk["dw"]]
+        od = decode_options(dw)
+        n, h, w_, cin = self._shape(blk["src"])
+        _, oh, ow, ce = self._shape(dw.outputs[0])
+        cout = self._shape(proj.outputs[0])[3]
+        k, s = self._shape(dw.inputs[1])[1], od["stride_h"]
+        pt, pl = _same_pads(h, w_, oh, ow, k, k, s, s) if od["padding"] == "same" else (0, 0)
+        act_e = (ACT[decode_options(ops[blk["expand"]])["fused_activation"]]
+                 if blk["expand"] is not None else 0)
+        return [n, cin, h, w_, ce, cout, oh, ow, k, s, pt, pl,
+                0 if blk["expand"] is None else 1, act_e, ACT[od["fused_activation"]],
+                n * oh * ow * cout]
+
+    def _block_plan(self, proj: Operator, blk: dict):
+        """shp_block_plan of the chain, or None if the fused kernel does not take it."""
+        import ctypes as C
+        from ._lib import lib
+        push = self._block_push(proj, blk)
+        out = (C.c_int32 * 8)()
+        if lib().shp_block_plan((C.c_int32 * 16)(*push), 16, out) != 0:
+            return None
+        return list(out)
+
+    def _block_weights(self, proj: Operator, blk: dict):
+        """The packed weights of a fused block (the operators' tensors back to back),
+        uploaded once."""
+        key = ("block", proj.index)
+        if key not in self.packed:
+            parts = []
+            for oi in (blk["expand"], blk["dw"], proj.index):
+                if oi is None:
+                    continue
+                op = self.model.operators[oi]
+                w = self.consts[op.inputs[1]].astype(np.float32)
+                n_out = self._shape(op.inputs[1])[0 if op.builtin == "CONV_2D" else 3]
+                b = (self.consts[op.inputs[2]].astype(np.float32)
+                     if len(op.inputs) > 2 and op.inputs[2] >= 0 else np.zeros(n_out, np.float32))
+                parts += [w.reshape(-1), b.reshape(-1)]
+            t = self.ctx.tensor(np.concatenate(parts))
+            self.owned.append(t)
+            self.packed[key] = t
+        return self.packed[key]
+
+    def _residual_epilogue(self, op: Operator, out_idx: int, act: str):
+        """(output tensor, residual, activation) of a CONV_2D, with its residual ADD folded in."""
+        if op.index not in self.residual_adds:
+            return out_idx, None, act
+        add_i, r_idx = self.residual_adds[op.index]
+        add = self.model.operators[add_i]
+        return add.outputs[0], self._get(r_idx), decode_options(add).get("fused_activation", "none")
+
+    def _run_block(self, proj: Operator, blk: dict) -> None:
+        out_idx, residual, act = self._residual_epilogue(
+            proj, proj.outputs[0], decode_options(proj)["fused_activation"])
+        y = self._alloc(out_idx)
+        self._launch("inverted_residual_nhwc", self._get(blk["src"]),
+                     self._block_weights(proj, blk), y, self._block_push(proj, blk), act=act,
+                     residual=residual)
 
     # -- helpers
     def _shape(self, idx: int) -> List[int]:
@@ -759,14 +883,21 @@ class TfliteExecutor:
 
     def _run_ops(self) -> None:
         self.op_log = []  # the dispatches of this run
-        fused_adds = {a: c for c, (a, _) in self.residual_adds.items()}
+        fused = {a: c for c, (a, _) in self.residual_adds.items()}
+        for pi, blk in self.blocks.items():
+            fused[blk["dw"]] = pi
+            if blk["expand"] is not None:
+                fused[blk["expand"]] = pi
         for oi in self.order:
             op = self.model.operators[oi]
             self.op_log.append({"index": op.index, "op": op.builtin,
                                 "options": decode_options(op), "inputs": op.inputs,
                                 "outputs": op.outputs, "dispatches": []})
-            if op.index in fused_adds:
-                self.op_log[-1]["fused_into"] = fused_adds[op.index]
+            if op.index in fused:
+                self.op_log[-1]["fused_into"] = fused[op.index]
+                continue
+            if op.index in self.blocks:
+                self._run_block(op, self.blocks[op.index])
                 continue
             self._run_op(op, self.op_log[-1]["options"])
 
@@ -811,13 +942,8 @@ class TfliteExecutor:
             fused = act if act in ("none", "relu", "relu6", "tanh") else None
             if fused is None:
                 raise ValueError(f"operator {op.index}: fused activation {act} not supported")
-            residual = None
-            if op.index in self.residual_adds:  # conv + bias + residual, then the ADD's act
-                add_i, r_idx = self.residual_adds[op.index]
-                add = self.model.operators[add_i]
-                out_idx = add.outputs[0]
-                residual = self._get(r_idx)
-                fused = decode_options(add).get("fused_activation", "none")
+            # conv + bias + residual, then the ADD's act
+            out_idx, residual, fused = self._residual_epilogue(op, out_idx, fused)
             y = self._alloc(out_idx)
             self._launch("conv2d_nhwc", self._get(ins[0]), w, y,
                          [n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw,
@@ -969,45 +1095,77 @@ _ACT_TO_TFL = {0: 0, 1: 1, 2: 3, 5: 4}  # registry epilogue code -> ActivationFu
 
 def model_to_tflite(m, description: str = "") -> bytes:
     """A TFL3 file of a resident model graph built on the TFLite path (MobileNetV2,
-    EfficientNet-Lite0: conv2d_nhwc, depthwise_conv2d_nhwc, global_avg_pool_nhwc,
-    fully_connected, softmax1000), with its weights: CONV_2D / DEPTHWISE_CONV_2D (OHWI and
-    [1,KH,KW,C] weights with separate bias tensors), ADD for a residual the graph fuses into
+    EfficientNet-Lite0: conv2d_nhwc, depthwise_conv2d_nhwc or the fused
+    inverted_residual_nhwc, global_avg_pool_nhwc, fully_connected, softmax1000), with its
+    weights: CONV_2D / DEPTHWISE_CONV_2D (OHWI and [1,KH,KW,C] weights with separate bias
+    tensors; a fused block as its three operators), ADD for a residual the graph fuses into
     a convolution, MEAN over H and W, FULLY_CONNECTED, SOFTMAX."""
     w = TfliteWriter(description or f"{m.arch} exported from the resident graph")
     tfl: Dict[int, int] = {}          # model tensor id -> tflite tensor index
-    shapes: Dict[int, List[int]] = {}
     host = lambda tid: m.download(tid)
+
+    def conv(label, x, n, ic, oh, ow, oc, k, s, same, wts, bias, act, residual=None):
+        wt = w.tensor(f"{label}/weights", [oc, k, k, ic], wts)
+        bt = w.tensor(f"{label}/bias", [oc], bias)
+        y = w.tensor(label, [n, oh, ow, oc])
+        opts = {0: ("b", 0 if same else 1), 1: ("i", s), 2: ("i", s),
+                3: ("b", 0 if residual is not None else act)}
+        w.op("CONV_2D", [x, wt, bt], [y], "Conv2DOptions", opts)
+        if residual is not None:
+            z = w.tensor(label + "/add", [n, oh, ow, oc])
+            w.op("ADD", [y, residual], [z], "AddOptions", {0: ("b", act)})
+            y = z
+        return y
+
+    def depthwise(label, x, n, c, oh, ow, k, s, same, wts, bias, act, dh=1, dw=1):
+        wt = w.tensor(f"{label}/weights", [1, k, k, c], wts)
+        bt = w.tensor(f"{label}/bias", [c], bias)
+        y = w.tensor(label, [n, oh, ow, c])
+        opts = {0: ("b", 0 if same else 1), 1: ("i", s), 2: ("i", s), 3: ("i", 1),
+                4: ("b", act), 5: ("i", dw), 6: ("i", dh)}
+        w.op("DEPTHWISE_CONV_2D", [x, wt, bt], [y], "DepthwiseConv2DOptions", opts)
+        return y
+
+    def model_input(tid, shape):
+        if tid not in tfl:
+            tfl[tid] = w.tensor("input", shape)
+            w.inputs.append(tfl[tid])
+        return tfl[tid]
+
     for k, op in enumerate(m.ops()):
         q = op.push
         if op.kernel == "conv2d_nhwc":
             n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, same = q[:12]
-            if op.in0 not in tfl:
-                tfl[op.in0] = w.tensor("input", [n, ih, iw, ic])
-                w.inputs.append(tfl[op.in0])
+            if kh != kw or sh != sw:
+                raise ValueError(f"op {k} ({op.label}): only square kernels and strides export")
+            x = model_input(op.in0, [n, ih, iw, ic])
             packed = host(op.in1)
             K = kh * kw * ic
-            wt = w.tensor(f"{op.label}/weights", [oc, kh, kw, ic], packed[:oc * K])
-            bt = w.tensor(f"{op.label}/bias", [oc], packed[oc * K:oc * K + oc])
-            act = _ACT_TO_TFL[op.act]
-            y = w.tensor(op.label, [n, oh, ow, oc])
-            opts = {0: ("b", 0 if same else 1), 1: ("i", sw), 2: ("i", sh),
-                    3: ("b", 0 if op.residual >= 0 else act)}
-            w.op("CONV_2D", [tfl[op.in0], wt, bt], [y], "Conv2DOptions", opts)
-            if op.residual >= 0:
-                z = w.tensor(op.label + "/add", [n, oh, ow, oc])
-                w.op("ADD", [y, tfl[op.residual]], [z], "AddOptions", {0: ("b", act)})
-                y = z
-            tfl[op.out] = y
+            tfl[op.out] = conv(op.label, x, n, ic, oh, ow, oc, kh, sh, same, packed[:oc * K],
+                               packed[oc * K:oc * K + oc], _ACT_TO_TFL[op.act],
+                               tfl[op.residual] if op.residual >= 0 else None)
         elif op.kernel == "depthwise_conv2d_nhwc":
             n, c, ih, iw, oh, ow, kh, kw, sh, sw, same, pt, pl, dh, dw = q[:15]
             packed = host(op.in1)
-            wt = w.tensor(f"{op.label}/weights", [1, kh, kw, c], packed[:kh * kw * c])
-            bt = w.tensor(f"{op.label}/bias", [c], packed[kh * kw * c:kh * kw * c + c])
-            y = w.tensor(op.label, [n, oh, ow, c])
-            opts = {0: ("b", 0 if same else 1), 1: ("i", sw), 2: ("i", sh), 3: ("i", 1),
-                    4: ("b", _ACT_TO_TFL[op.act]), 5: ("i", dw), 6: ("i", dh)}
-            w.op("DEPTHWISE_CONV_2D", [tfl[op.in0], wt, bt], [y], "DepthwiseConv2DOptions", opts)
-            tfl[op.out] = y
+            tfl[op.out] = depthwise(op.label, tfl[op.in0], n, c, oh, ow, kh, sh, same,
+                                    packed[:kh * kw * c], packed[kh * kw * c:kh * kw * c + c],
+                                    _ACT_TO_TFL[op.act], dh, dw)
+        elif op.kernel == "inverted_residual_nhwc":
+            n, cin, h, w_, ce, cout, oh, ow, kk, s, pt, pl, expand, act_e, act_d = q[:15]
+            packed, o = host(op.in1), 0
+            x = model_input(op.in0, [n, h, w_, cin])
+            base = op.label[:-len("_mbconv")] if op.label.endswith("_mbconv") else op.label
+            if expand:
+                x = conv(f"{base}_expand", x, n, cin, h, w_, ce, 1, 1, True,
+                         packed[:ce * cin], packed[ce * cin:ce * cin + ce], _ACT_TO_TFL[act_e])
+                o = ce * cin + ce
+            x = depthwise(f"{base}_depthwise", x, n, ce, oh, ow, kk, s, True,
+                          packed[o:o + kk * kk * ce], packed[o + kk * kk * ce:o + kk * kk * ce + ce],
+                          _ACT_TO_TFL[act_d])
+            o += kk * kk * ce + ce
+            tfl[op.out] = conv(f"{base}_project", x, n, ce, oh, ow, cout, 1, 1, True,
+                               packed[o:o + cout * ce], packed[o + cout * ce:o + cout * ce + cout],
+                               _ACT_TO_TFL[op.act], tfl[op.residual] if op.residual >= 0 else None)
         elif op.kernel == "global_avg_pool_nhwc":
             n, h, w_, c = q[:4]
             axes = w.tensor(f"{op.label}/axes", [2], np.array([1, 2], np.int32).view(np.float32),

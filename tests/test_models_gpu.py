@@ -86,6 +86,32 @@ def test_cnn_per_op_and_top1(ctx, orc, arch, batch):
         assert_rankings_match(logits_gpu, host[out_logits], batch, arch)
 
 
+@pytest.mark.parametrize("arch,batch,fused_auto", [("mobilenet_v2", 1, 17),
+                                                   ("efficientnet_lite0", 8, 4)])
+def test_mbconv_blocks_fused_equal_three_operators(arch, batch, fused_auto):
+    """The same model (same seed, so the same weights) built three ways: every MBConv block
+    as one inverted_residual_nhwc launch, as the TFLite scheduler's three operators, and the
+    default (one launch where the library's plan query says it pays).  Per-op checks of each
+    fused block against the oracle's three-operator chain at 1e-4 run in
+    test_cnn_per_op_and_top1; here the whole forwards must agree."""
+    from spirv_inference_amd import Context
+    from spirv_inference_amd.models import Model
+    outs, counts = {}, {}
+    for mode, fuse in (("three", -1), ("auto", 0), ("always", 1)):
+        with Context("any") as c:
+            c.tune("ir_fuse", fuse)
+            with Model(c, arch, batch, seed=2) as m:
+                counts[mode] = sum(op.kernel == "inverted_residual_nhwc" for op in m.ops())
+                m.run()
+                c.sync()
+                outs[mode] = (m.output(1).download(), m.output(0).download())
+    print(f"[{arch} b{batch}] fused blocks: {counts}", flush=True)
+    assert counts == {"three": 0, "auto": fused_auto, "always": 17 if arch == "mobilenet_v2" else 16}
+    for mode in ("auto", "always"):
+        assert_close(outs[mode][0], outs["three"][0], 1e-4, 1e-4, f"{arch} logits {mode}")
+        assert_close(outs[mode][1], outs["three"][1], 1e-6, 1e-4, f"{arch} probs {mode}")
+
+
 def test_resnet50_b32_headline_per_op(ctx, orc):
     """The headline config exactly as bench.py builds it (ResNet-50 v1.5, batch 32, seed 2):
     every one of its ops (the 53 convolutions with their b32 plans: 64x64/k16 tiles with 2-3

@@ -427,3 +427,43 @@ def test_compare_is_tensor_rs_comparator(orc):
     mm2, _, _ = orc.compare(a[:3], e, 0.25)           # two missing values
     assert mm2 == 1 + 2
     assert orc.compare(e, e, 0.0)[0] == 0
+
+
+@pytest.mark.parametrize("expand,k,s,res", [(True, 3, 2, False), (True, 5, 1, True),
+                                            (False, 3, 1, False), (True, 3, 1, True)])
+def test_inverted_residual_vs_float64(orc, expand, k, s, res):
+    """inverted_residual_nhwc (the three MBConv operators in one call) against a float64
+    numpy restatement of 1x1 conv + ReLU6, SAME-padded depthwise + ReLU6, 1x1 conv +
+    residual: closed-form einsums and an explicit tap loop, not the oracle's loops."""
+    rng = np.random.default_rng(3)
+    n, cin, h, w, cout = 2, 8, 9, 7, 8
+    ce = 32 if expand else cin
+    oh, ow = (h + s - 1) // s, (w + s - 1) // s
+    pt = max((oh - 1) * s + k - h, 0) // 2
+    pl = max((ow - 1) * s + k - w, 0) // 2
+    x = rng.standard_normal(n * h * w * cin).astype(np.float32)
+    parts = []
+    if expand:
+        we, be = rng.standard_normal((ce, cin)) * 0.3, rng.standard_normal(ce) * 0.1
+        parts += [we, be]
+    wd, bd = rng.standard_normal((k, k, ce)) * 0.3, rng.standard_normal(ce) * 0.1
+    wp, bp = rng.standard_normal((cout, ce)) * 0.2, rng.standard_normal(cout) * 0.1
+    parts += [wd, bd, wp, bp]
+    packed = np.concatenate([np.asarray(q, np.float32).reshape(-1) for q in parts])
+    total = n * oh * ow * cout
+    push = [n, cin, h, w, ce, cout, oh, ow, k, s, pt, pl, int(expand), 2, 2, total]
+    got = orc.run("inverted_residual_nhwc", x, packed, total, push,
+                  residual=x if res else None)
+    X = x.reshape(n, h, w, cin).astype(np.float64)
+    E = np.clip(np.einsum("nhwc,ec->nhwe", X, we) + be, 0, 6) if expand else X
+    Ep = np.zeros((n, h + 2 * k, w + 2 * k, ce))
+    Ep[:, pt:pt + h, pl:pl + w] = E
+    D = np.zeros((n, oh, ow, ce))
+    for ky in range(k):
+        for kx in range(k):
+            D += Ep[:, ky:ky + (oh - 1) * s + 1:s, kx:kx + (ow - 1) * s + 1:s] * wd[ky, kx]
+    D = np.clip(D + bd, 0, 6)
+    Y = np.einsum("nhwe,oe->nhwo", D, wp) + bp
+    if res:
+        Y = Y + X
+    assert_close(got, Y.reshape(-1), 2e-6, 2e-6, "inverted_residual_nhwc")

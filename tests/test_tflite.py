@@ -251,3 +251,88 @@ def test_executor_keeps_add_when_residual_comes_later():
         assert ex.residual_adds == {}
     else:
         assert conv in ex.residual_adds
+
+
+def _mbconv_model(cin=8, ce=32, cout=8, k=3, s=1, expand=True, residual=True, extra=None):
+    """x -> [1x1 CONV_2D relu6] -> DEPTHWISE k x k relu6 -> 1x1 CONV_2D -> [ADD x] with
+    variants that must not fuse (extra: 'expand_reader' reads the expanded tensor elsewhere,
+    'dw_output' makes the depthwise output a model output, 'dilated' dilates the depthwise,
+    'strided_expand' gives the expand stride 2)."""
+    rng = np.random.default_rng(0)
+    w = T.TfliteWriter()
+    h = 6
+    oh = (h + s - 1) // s
+    x = w.tensor("x", [1, h, h, cin])
+    w.inputs = [x]
+    src = x
+    ops = {}
+    if expand:
+        we = w.tensor("we", [ce, 1, 1, cin], rng.standard_normal(ce * cin).astype(np.float32))
+        be = w.tensor("be", [ce], rng.standard_normal(ce).astype(np.float32))
+        es = 2 if extra == "strided_expand" else 1
+        eh = (h + es - 1) // es
+        e = w.tensor("e", [1, eh, eh, ce])
+        ops["expand"] = w.op("CONV_2D", [x, we, be], [e], "Conv2DOptions",
+                             {0: ("b", 0), 1: ("i", es), 2: ("i", es), 3: ("b", 3)})
+        src, h = e, eh
+        oh = (h + s - 1) // s
+    else:
+        ce = cin
+    wd = w.tensor("wd", [1, k, k, ce], rng.standard_normal(k * k * ce).astype(np.float32))
+    bd = w.tensor("bd", [ce], rng.standard_normal(ce).astype(np.float32))
+    d = w.tensor("d", [1, oh, oh, ce])
+    dil = 2 if extra == "dilated" else 1
+    ops["dw"] = w.op("DEPTHWISE_CONV_2D", [src, wd, bd], [d], "DepthwiseConv2DOptions",
+                     {0: ("b", 0), 1: ("i", s), 2: ("i", s), 3: ("i", 1), 4: ("b", 3),
+                      5: ("i", dil), 6: ("i", dil)})
+    wp = w.tensor("wp", [cout, 1, 1, ce], rng.standard_normal(cout * ce).astype(np.float32))
+    y = w.tensor("y", [1, oh, oh, cout])
+    ops["project"] = w.op("CONV_2D", [d, wp, -1], [y], "Conv2DOptions",
+                          {0: ("b", 0), 1: ("i", 1), 2: ("i", 1), 3: ("b", 0)})
+    out = y
+    if residual and s == 1 and cin == cout and not (expand and extra == "strided_expand"):
+        z = w.tensor("z", [1, oh, oh, cout])
+        ops["add"] = w.op("ADD", [y, x], [z], "AddOptions", {0: ("b", 0)})
+        out = z
+    w.outputs = [out]
+    if extra == "expand_reader":
+        q = w.tensor("q", [1, h, h, ce])
+        w.op("NEG", [src], [q])
+        w.outputs.append(q)
+    if extra == "dw_output":
+        w.outputs.append(d)
+    return T.parse_model(w.finish()), ops
+
+
+@pytest.mark.parametrize("kw", [{}, {"expand": False, "cin": 16, "cout": 16},
+                                {"k": 5, "s": 2, "residual": False},
+                                {"cout": 12, "residual": False}])
+def test_executor_fuses_inverted_residual_chain(kw):
+    m, ops = _mbconv_model(**kw)
+    want = {"expand": ops.get("expand"), "dw": ops["dw"], "src": 0}
+    ex = T.TfliteExecutor(_NoDevice(), m, fuse_blocks=True)  # every chain the kernel takes
+    assert ex.blocks == {ops["project"]: want}
+    if "add" in ops:  # the projection still takes its residual ADD
+        assert ex.residual_adds == {ops["project"]: (ops["add"], 0)}
+    # by default where the plan query expects one launch to pay: blocks with an expand at
+    # this size (36 output pixels), not a depthwise + projection pair alone
+    auto = T.TfliteExecutor(_NoDevice(), m).blocks
+    assert auto == ({ops["project"]: want} if kw.get("expand", True) else {})
+    assert T.TfliteExecutor(_NoDevice(), m, fuse_blocks=False).blocks == {}
+
+
+@pytest.mark.parametrize("extra", ["expand_reader", "dw_output", "dilated", "strided_expand"])
+def test_executor_keeps_chains_it_cannot_fuse(extra):
+    m, ops = _mbconv_model(extra=extra)
+    ex = T.TfliteExecutor(_NoDevice(), m, fuse_blocks=True)
+    if extra in ("expand_reader", "strided_expand"):
+        # the depthwise and projection still fuse, reading the expanded tensor as the input
+        e_out = m.operators[ops["expand"]].outputs[0]
+        assert ex.blocks == {ops["project"]: {"expand": None, "dw": ops["dw"], "src": e_out}}
+    else:
+        assert ex.blocks == {}
+
+
+def test_executor_needs_channel_multiples_for_a_block():
+    m, _ = _mbconv_model(cin=6, ce=24, cout=6)  # cin % 4 != 0, ce % 16 != 0
+    assert T.TfliteExecutor(_NoDevice(), m, fuse_blocks=True).blocks == {}
