@@ -246,15 +246,33 @@ def bench_config(ctx, arch: str, batch: int, seq_len: int, steps: int):
         m.run()
     ctx.sync()
     ms = (time.perf_counter() - t0) / steps * 1e3
-    tfl = time_tflite_executor(ctx, m, steps) if arch in ("mobilenet_v2", "efficientnet_lite0") \
-        else None
+    cnn = arch in ("mobilenet_v2", "efficientnet_lite0")
+    tfl = time_tflite_executor(ctx, m, steps) if cnn else None
+    fused = sum(op.kernel == "inverted_residual_nhwc" for op in m.ops())
     m.close()
     tflops = flops / (ms / 1e3) / 1e12
-    return {"batch": batch, "seq_len": seq_len or None, "ms_per_forward": round(ms, 4),
-            "gflop_per_forward": round(flops / 1e9, 3), "weight_mb": round(wbytes / 1e6, 2),
-            "achieved_tflops": round(tflops, 3),
-            "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
-            "tflite_executor": tfl}
+    out = {"batch": batch, "seq_len": seq_len or None, "ms_per_forward": round(ms, 4),
+           "gflop_per_forward": round(flops / 1e9, 3), "weight_mb": round(wbytes / 1e6, 2),
+           "achieved_tflops": round(tflops, 3),
+           "frac_fp32_mfma": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+           "tflite_executor": tfl}
+    if cnn:  # the same graph with every MBConv block as the TFLite scheduler's three operators
+        from spirv_inference_amd import Context
+        with Context("any") as c3:
+            c3.tune("ir_fuse", -1)
+            m3 = Model(c3, arch, batch, seq_len, seed=2)
+            m3.use_graph(True)
+            for _ in range(3):
+                m3.run()
+            c3.sync()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m3.run()
+            c3.sync()
+            out["mbconv_blocks_fused"] = fused
+            out["three_operator_ms_per_forward"] = round((time.perf_counter() - t0) / steps * 1e3, 4)
+            m3.close()
+    return out
 
 
 def time_tflite_executor(ctx, m, steps: int):
@@ -471,6 +489,9 @@ def main() -> int:
             c = configs[arch]
             log(f"{arch} b{b}: {c['ms_per_forward']:.3f} ms/forward, "
                 f"{c['achieved_tflops']:.1f} TFLOP/s ({100 * c['frac_fp32_mfma']:.1f}% of fp32 MFMA)")
+            if "three_operator_ms_per_forward" in c:
+                log(f"{arch} b{b}: {c['mbconv_blocks_fused']} MBConv blocks fused; with every "
+                    f"block as three launches {c['three_operator_ms_per_forward']:.3f} ms/forward")
             if c["tflite_executor"]:
                 t = c["tflite_executor"]
                 log(f"{arch} b{b} via the TFLite executor: {t['graph_ms_per_forward']:.3f} ms "
