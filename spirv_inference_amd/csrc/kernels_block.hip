@@ -69,55 +69,40 @@ struct IrArgs {
                                    // 16-row blocks of the output tile
     int o_x, o_w, o_be, o_wd, o_bd, o_e, o_d, o_wp, o_hv, o_flag;  // LDS offsets (floats)
     int w_we, w_be, w_wd, w_bd, w_wp, w_bp;                        // packed-weight offsets
-    // ceil(2^32 / d) for the divisors cin / 4, cin16 / 4, hw and tw: n / d = umulhi(n, m)
-    // exactly for n * d < 2^32
-    unsigned m_cin4, m_c4n, m_hw, m_tw;
+    // ceil(2^32 / d) for the divisors cin / 4, cin16 / 4, hw, tw, S, J, tiles_x and tiles_y:
+    // n / d = umulhi(n, m) exactly for n * d < 2^32
+    unsigned m_cin4, m_c4n, m_hw, m_tw, m_S, m_J, m_tx, m_ty;
 };
 
 __device__ __forceinline__ int udiv(int n, unsigned m) {
     return m ? (int)__umulhi((unsigned)n, m) : n;  // m = 0 stands for d = 1
 }
 
-// The idx-th float4 of one chunk's weights: We rows, be, Wd taps, bd, then the Wp rows of
-// this output-channel slice (each 32 channels = 8 float4 wide, the We rows cin wide).
+// The idx-th float4 of one chunk's weights: the We rows (cin wide), then rows of 32 channels
+// (8 float4): be (with expand), the k*k Wd taps, bd, the Wp rows of this output-channel
+// slice.  In the packed buffer be, the taps and bd sit ce apart from w_be (= w_wd - ce
+// without expand) and the Wp rows follow; in LDS be, the taps and bd are 32 apart from o_be
+// and the Wp rows WPS apart from o_wp, so a slot is a few selects, not a chain of branches.
 // goff: packed-weight offset at chunk 0; meta: LDS offset | channel within the chunk << 16
 // | 1 << 24 for the We rows (which advance 32 rows per chunk; the rest 32 channels).
 template <int K>
 __device__ __forceinline__ void weight_slot(const IrArgs& a, int j, int idx, int& goff,
                                             int& meta) {
-    if (a.expand) {
-        const int cin4 = a.cin >> 2;
-        const int nwe = CC * cin4;
-        if (idx < nwe) {  // the chunk's We rows are one contiguous span
-            const int r = udiv(idx, a.m_cin4), q = idx - r * cin4;
-            goff = a.w_we + 4 * idx;
-            meta = (a.o_w + r * a.wsx + 4 * q) | (r << 16) | (1 << 24);
-            return;
-        }
-        idx -= nwe;
-        if (idx < 8) {
-            goff = a.w_be + 4 * idx;
-            meta = (a.o_be + 4 * idx) | ((4 * idx) << 16);
-            return;
-        }
-        idx -= 8;
-    }
-    if (idx < 8 * K * K) {
-        const int t = idx >> 3, q = idx & 7;
-        goff = a.w_wd + t * a.ce + 4 * q;
-        meta = (a.o_wd + t * CC + 4 * q) | ((4 * q) << 16);
-        return;
-    }
-    idx -= 8 * K * K;
-    if (idx < 8) {
-        goff = a.w_bd + 4 * idx;
-        meta = (a.o_bd + 4 * idx) | ((4 * idx) << 16);
-        return;
-    }
-    idx -= 8;
-    const int r = idx >> 3, q = idx & 7;
-    goff = a.w_wp + (j * a.coj + r) * a.ce + 4 * q;
-    meta = (a.o_wp + r * WPS + 4 * q) | ((4 * q) << 16);
+    const int nwe = a.expand ? CC * (a.cin >> 2) : 0;
+    // We rows
+    const int r = udiv(idx, a.m_cin4), q = idx - r * (a.cin >> 2);
+    const int g_we = a.w_we + 4 * idx, l_we = a.o_w + r * a.wsx + 4 * q;
+    // 32-channel rows: row 0 = be (a virtual row before the taps without expand)
+    const int i8 = idx - nwe;
+    const int row = (i8 >> 3) + (a.expand ? 0 : 1), q8 = i8 & 7;
+    const bool wp = row >= K * K + 2;
+    const int rp = row - (K * K + 2);
+    const int base = a.w_wd - a.ce;  // be's offset (w_be with expand)
+    const int g_row = base + (row + (wp ? j * a.coj : 0)) * a.ce + 4 * q8;
+    const int l_row = wp ? a.o_wp + rp * WPS + 4 * q8 : a.o_be + row * CC + 4 * q8;
+    const bool we = idx < nwe;
+    goff = we ? g_we : g_row;
+    meta = we ? (l_we | (r << 16) | (1 << 24)) : (l_row | ((4 * q8) << 16));
 }
 
 // Loads (fetch) and LDS stores (put) of this thread's float4s of one chunk's weights,
@@ -169,14 +154,11 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, li = lane & 15;
-    int id = blockIdx.x;
-    const int si = id % a.S;
-    id /= a.S;
-    const int j = id % a.J;
-    const int tile = id / a.J;  // (img, ty, tx) row-major
-    const int tx = tile % a.tiles_x;
-    const int ty = (tile / a.tiles_x) % a.tiles_y;
-    const int img = tile / (a.tiles_x * a.tiles_y);
+    const int id = blockIdx.x;
+    const int q_s = udiv(id, a.m_S), si = id - q_s * a.S;
+    const int tile = udiv(q_s, a.m_J), j = q_s - tile * a.J;  // tile: (img, ty, tx) row-major
+    const int q_x = udiv(tile, a.m_tx), tx = tile - q_x * a.tiles_x;
+    const int img = udiv(q_x, a.m_ty), ty = q_x - img * a.tiles_y;
     const int oy0 = ty * a.th, ox0 = tx * a.tw;
     const int iy0 = oy0 * ST - a.pt, ix0 = ox0 * ST - a.pl;
     const int c_begin = si * a.cpw;
@@ -518,6 +500,9 @@ IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
 bool geometry_ok(const IrGeom& g) {
     return g.lds_floats * 4 <= kMaxLds && g.nbw <= 20 && g.nf_max <= 256 * NPF &&
            (int64_t)g.S * g.nblk * 1024 < (1ll << 31) &&
+           // the kernel's multiply-high divisions of the workgroup id stay exact
+           (int64_t)g.tiles * g.J * g.S *
+                   std::max(std::max(g.S, g.J), std::max(g.tiles_x, g.tiles_y)) < (1ll << 32) &&
            (g.S == 1 || (int64_t)g.tiles * g.J <= (int64_t)(shp::kSplitCounterBytes / sizeof(int))) &&
            (int64_t)g.tiles * g.J * g.S < (1ll << 31);
 }
@@ -761,6 +746,10 @@ int launch_ir(const shp::Launch& l) {
     a.m_c4n = magic(g.cin16 / 4);
     a.m_hw = magic(g.hw);
     a.m_tw = magic(pl.tw);
+    a.m_S = magic(g.S);
+    a.m_J = magic(g.J);
+    a.m_tx = magic(g.tiles_x);
+    a.m_ty = magic(g.tiles_y);
     int o = 0;
     if (sh.expand) {
         a.w_we = 0;
