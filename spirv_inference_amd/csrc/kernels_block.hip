@@ -50,6 +50,28 @@ constexpr int WPS = CC + 4;  // of the projection weight chunk
 constexpr int NPF = 12;      // float4 weight loads per thread and chunk, at most
 constexpr int kMaxLds = 160 * 1024;
 
+// LDS layout (float offsets) of one workgroup, shared by the host plan and the kernel:
+// halo patch | We chunk | be | Wd taps | bd | E | D | Wp chunk | halo-row validity | flag.
+struct IrLds {
+    int x, w, be, wd, bd, e, d, wp, hv, flag, total;
+};
+__host__ __device__ inline IrLds ir_lds(int hpb, int xs, int expand, int k, int pb, int ob) {
+    IrLds l;
+    int o = 0;
+    l.x = o;    o += hpb * 16 * xs;
+    l.w = o;    o += expand ? CC * xs : 0;
+    l.be = o;   o += CC;
+    l.wd = o;   o += k * k * CC;
+    l.bd = o;   o += CC;
+    l.e = o;    o += expand ? hpb * 16 * ES : 0;
+    l.d = o;    o += pb * 16 * DS;
+    l.wp = o;   o += ob * 16 * WPS;
+    l.hv = o;   o += hpb * 16;
+    l.flag = o; o += 4;
+    l.total = o;
+    return l;
+}
+
 struct IrArgs {
     const float* x;
     const float* w;
@@ -62,13 +84,12 @@ struct IrArgs {
     float alpha;
     int th, tw, tiles_y, tiles_x;  // output tile and the tile grid of one image
     int hw, hp, hpb;               // halo columns, halo pixels, 16-row blocks of them
-    int cin16, xs, wsx;            // cin rounded up to 16; LDS row strides of x and We
+    int cin16, xs;                 // cin rounded up to 16; LDS row stride of x and We
     int nchunk, cpw, S;            // 32-channel chunks of ce (the last may hold 16),
                                    // chunks per split, splits
     int J, coj, ob, pb;            // output-channel splits, channels per split (16 * ob),
                                    // 16-row blocks of the output tile
-    int o_x, o_w, o_be, o_wd, o_bd, o_e, o_d, o_wp, o_hv, o_flag;  // LDS offsets (floats)
-    int w_we, w_be, w_wd, w_bd, w_wp, w_bp;                        // packed-weight offsets
+    int w_wd;  // packed-weight offset of the depthwise taps (ce * (cin + 1) with expand, else 0)
     // ceil(2^32 / d) for the divisors cin / 4, cin16 / 4, hw, tw, S, J, tiles_x and tiles_y:
     // n / d = umulhi(n, m) exactly for n * d < 2^32
     unsigned m_cin4, m_c4n, m_hw, m_tw, m_S, m_J, m_tx, m_ty;
@@ -86,12 +107,12 @@ __device__ __forceinline__ int udiv(int n, unsigned m) {
 // goff: packed-weight offset at chunk 0; meta: LDS offset | channel within the chunk << 16
 // | 1 << 24 for the We rows (which advance 32 rows per chunk; the rest 32 channels).
 template <int K>
-__device__ __forceinline__ void weight_slot(const IrArgs& a, int j, int idx, int& goff,
-                                            int& meta) {
+__device__ __forceinline__ void weight_slot(const IrArgs& a, const IrLds& L, int j, int idx,
+                                            int& goff, int& meta) {
     const int nwe = a.expand ? CC * (a.cin >> 2) : 0;
-    // We rows
+    // We rows (at the start of the packed buffer)
     const int r = udiv(idx, a.m_cin4), q = idx - r * (a.cin >> 2);
-    const int g_we = a.w_we + 4 * idx, l_we = a.o_w + r * a.wsx + 4 * q;
+    const int g_we = 4 * idx, l_we = L.w + r * a.xs + 4 * q;
     // 32-channel rows: row 0 = be (a virtual row before the taps without expand)
     const int i8 = idx - nwe;
     const int row = (i8 >> 3) + (a.expand ? 0 : 1), q8 = i8 & 7;
@@ -99,7 +120,7 @@ __device__ __forceinline__ void weight_slot(const IrArgs& a, int j, int idx, int
     const int rp = row - (K * K + 2);
     const int base = a.w_wd - a.ce;  // be's offset (w_be with expand)
     const int g_row = base + (row + (wp ? j * a.coj : 0)) * a.ce + 4 * q8;
-    const int l_row = wp ? a.o_wp + rp * WPS + 4 * q8 : a.o_be + row * CC + 4 * q8;
+    const int l_row = wp ? L.wp + rp * WPS + 4 * q8 : L.be + row * CC + 4 * q8;
     const bool we = idx < nwe;
     goff = we ? g_we : g_row;
     meta = we ? (l_we | (r << 16) | (1 << 24)) : (l_row | ((4 * q8) << 16));
@@ -169,56 +190,65 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     const int nblk = a.pb * a.ob;
     const int hrows = a.hpb * 16;
 
-    float* Xs = lds + a.o_x;
-    float* Ws = lds + a.o_w;
-    const float* Bes = lds + a.o_be;
-    const float* Wds = lds + a.o_wd;
-    const float* Bds = lds + a.o_bd;
-    float* Es = lds + a.o_e;
-    float* Ds = lds + a.o_d;
-    float* Wps = lds + a.o_wp;
-    int* hvalid = reinterpret_cast<int*>(lds + a.o_hv);  // halo row inside the image
+    const IrLds L = ir_lds(a.hpb, a.xs, a.expand, K, a.pb, a.ob);
+    float* Xs = lds + L.x;
+    float* Ws = lds + L.w;
+    const float* Bes = lds + L.be;
+    const float* Wds = lds + L.wd;
+    const float* Bds = lds + L.bd;
+    float* Es = lds + L.e;
+    float* Ds = lds + L.d;
+    float* Wps = lds + L.wp;
+    int* hvalid = reinterpret_cast<int*>(lds + L.hv);  // halo row inside the image
+
+    // halo patch of x: hrows rows (halo pixels, row-major) of cin16 floats; zero outside
+    // the image, in the padding columns and in the rows past the patch.  8 float4 loads per
+    // thread per batch; the first batch is issued before the weight slots are set up and
+    // stored after the first chunk's weight loads are issued, so the two overlap.
+    const int c4n = a.cin16 >> 2;
+    const int xtotal = hrows * c4n;
+    f4v xv[8];
+    int xd[8];
+    auto load_x = [&](int e0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int e = e0 + 256 * t;
+            xv[t] = f4v{0.f, 0.f, 0.f, 0.f};
+            xd[t] = -1;
+            if (e < xtotal) {
+                const int r = udiv(e, a.m_c4n), q = e - r * c4n;
+                xd[t] = r * a.xs + 4 * q;
+                if (r < a.hp && 4 * q < a.cin) {
+                    const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+                    const int iy = iy0 + hy, ix = ix0 + hx;
+                    if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_)
+                        xv[t] = *reinterpret_cast<const f4v*>(
+                            a.x + (((int64_t)img * a.h + iy) * a.w_ + ix) * a.cin + 4 * q);
+                }
+            }
+        }
+    };
+    auto store_x = [&]() {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            if (xd[t] >= 0) *reinterpret_cast<f4v*>(Xs + xd[t]) = xv[t];
+    };
+    load_x(tid);
 
     // this thread's share of every chunk's weights, and the first chunk's loads
     int goff[NPF], meta[NPF];
 #pragma unroll
     for (int u = 0; u < NPF; ++u) {
         goff[u] = meta[u] = 0;
-        if (tid + 256 * u < nf) weight_slot<K>(a, j, tid + 256 * u, goff[u], meta[u]);
+        if (tid + 256 * u < nf) weight_slot<K>(a, L, j, tid + 256 * u, goff[u], meta[u]);
     }
     f4v pf[NPF];  // (native vectors: HIP's float4 struct copies would pin them to scratch)
     fetch_weights<0>(pf, a, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
 
-    // halo patch of x: hrows rows (halo pixels, row-major) of cin16 floats; zero outside
-    // the image, in the padding columns and in the rows past the patch (8 loads in flight
-    // per thread)
-    {
-        const int c4n = a.cin16 >> 2;
-        const int total = hrows * c4n;
-        for (int e0 = tid; e0 < total; e0 += 2048) {
-            f4v v[8];
-            int dst[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int e = e0 + 256 * t;
-                v[t] = f4v{0.f, 0.f, 0.f, 0.f};
-                dst[t] = -1;
-                if (e < total) {
-                    const int r = udiv(e, a.m_c4n), q = e - r * c4n;
-                    dst[t] = r * a.xs + 4 * q;
-                    if (r < a.hp && 4 * q < a.cin) {
-                        const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
-                        const int iy = iy0 + hy, ix = ix0 + hx;
-                        if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_)
-                            v[t] = *reinterpret_cast<const f4v*>(
-                                a.x + (((int64_t)img * a.h + iy) * a.w_ + ix) * a.cin + 4 * q);
-                    }
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                if (dst[t] >= 0) *reinterpret_cast<f4v*>(Xs + dst[t]) = v[t];
-        }
+    store_x();
+    for (int e0 = tid + 2048; e0 < xtotal; e0 += 2048) {  // patches of more than 2048 float4
+        load_x(e0);
+        store_x();
     }
     for (int r = tid; r < hrows; r += 256) {
         const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
@@ -229,7 +259,7 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     // the depthwise rows past the tile's pixels (read by the projection as zeros)
     if (a.expand && a.cin16 > a.cin) {
         const int pc = a.cin16 - a.cin;
-        for (int e = tid; e < CC * pc; e += 256) Ws[(e / pc) * a.wsx + a.cin + e % pc] = 0.f;
+        for (int e = tid; e < CC * pc; e += 256) Ws[(e / pc) * a.xs + a.cin + e % pc] = 0.f;
     }
     for (int e = tid; e < (a.ob * 16 - cv) * CC; e += 256)
         Wps[(cv + e / CC) * WPS + e % CC] = 0.f;
@@ -256,8 +286,8 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
             const int Q = a.cin16 >> 2;
             const ActClamp act_e(a.act_e);
             const float be0 = Bes[li], be1 = Bes[16 + li];
-            const float* wb0 = Ws + li * a.wsx + g * Q;
-            const float* wb1 = wb0 + 16 * a.wsx;
+            const float* wb0 = Ws + li * a.xs + g * Q;
+            const float* wb1 = wb0 + 16 * a.xs;
             for (int hb = wave; hb < a.hpb; hb += 8) {  // row blocks hb and hb + 4
                 const bool two = hb + 4 < a.hpb;
                 const float* xa0 = Xs + (hb * 16 + li) * a.xs + g * Q;
@@ -362,7 +392,7 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         const int oo = obi * 16 + (l & 15);
         if (oo >= cv) return;
         const int o = j * a.coj + oo;
-        const float bias = a.w[a.w_bp + o];
+        const float bias = a.w[a.w_wd + (K * K + 1 + a.cout) * a.ce + o];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int p = pbi * 16 + 4 * (l >> 4) + r;
@@ -397,15 +427,32 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are stored
     __syncthreads();
-    int* flag = reinterpret_cast<int*>(lds + a.o_flag);
+    int* flag = reinterpret_cast<int*>(lds + L.flag);
     int* cnt = a.counters + slot;
     if (tid == 0)
         *flag = __hip_atomic_fetch_add((SHP_GLOBAL int*)cnt, 1, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT) == a.S - 1;
     __syncthreads();
     if (!*flag) return;
-    // the last arrival: every thread sums up to 2 positions over the splits, in split order,
-    // with 8 splits x 2 positions of loads in flight, and stores their outputs
+    // the last arrival: every thread sums its positions over the splits, in split order, and
+    // stores their outputs; one position with up to 16 splits of loads in flight where the
+    // tile fits one pass, else 2 positions x 8 splits
+    if (W <= 256) {
+        if (tid < W) {
+            f4v t = f4v{0.f, 0.f, 0.f, 0.f};
+            for (int s0 = 0; s0 < a.S; s0 += 16) {
+                float4 q[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (s0 + u < a.S)
+                        q[u] = ld_coh16(prs, (unsigned)(((s0 + u) * W + tid) * 16), 0);
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (s0 + u < a.S) t += f4v{q[u].x, q[u].y, q[u].z, q[u].w};
+            }
+            store(tid >> 6, tid & 63, floatx4{t.x, t.y, t.z, t.w});
+        }
+    } else
     for (int f0 = tid; f0 < W; f0 += 512) {
         f4v t[2];
 #pragma unroll
@@ -454,9 +501,8 @@ int row_stride(int c16) { return c16 + (36 - c16 % 32) % 32; }
 
 // Derived sizes of one plan (everything the kernel arguments need except pointers).
 struct IrGeom {
-    int tiles_y, tiles_x, tiles, hh, hw, hp, hpb, cin16, xs, wsx, nchunk, cpw, S, J, coj, ob, pb;
+    int tiles_y, tiles_x, tiles, hh, hw, hp, hpb, cin16, xs, nchunk, cpw, S, J, coj, ob, pb;
     int nblk, nbw, nf_max, lds_floats;
-    int o_x, o_w, o_be, o_wd, o_bd, o_e, o_d, o_wp, o_hv, o_flag;
 };
 
 IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
@@ -470,7 +516,6 @@ IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
     g.hpb = ceil_div(g.hp, 16);
     g.cin16 = ceil_div(sh.cin, 16) * 16;
     g.xs = row_stride(g.cin16);
-    g.wsx = g.xs;
     g.nchunk = ceil_div(sh.ce, CC);
     g.cpw = ceil_div(g.nchunk, std::max(1, std::min(S, g.nchunk)));
     g.S = ceil_div(g.nchunk, g.cpw);  // no empty split
@@ -482,18 +527,7 @@ IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
     g.nblk = g.pb * g.ob;
     g.nbw = ceil_div(g.nblk, 4);
     g.nf_max = (sh.expand ? CC * (sh.cin / 4) + 8 : 0) + 8 * sh.k * sh.k + 8 + 8 * g.coj;
-    int o = 0;
-    g.o_x = o;   o += g.hpb * 16 * g.xs;
-    g.o_w = o;   o += sh.expand ? CC * g.wsx : 0;
-    g.o_be = o;  o += CC;
-    g.o_wd = o;  o += sh.k * sh.k * CC;
-    g.o_bd = o;  o += CC;
-    g.o_e = o;   o += sh.expand ? g.hpb * 16 * ES : 0;
-    g.o_d = o;   o += g.pb * 16 * DS;
-    g.o_wp = o;  o += g.ob * 16 * WPS;
-    g.o_hv = o;  o += g.hpb * 16;
-    g.o_flag = o; o += 4;
-    g.lds_floats = o;
+    g.lds_floats = ir_lds(g.hpb, g.xs, sh.expand, sh.k, g.pb, g.ob).total;
     return g;
 }
 
@@ -736,11 +770,9 @@ int launch_ir(const shp::Launch& l) {
     a.alpha = l.epi->alpha;
     a.th = pl.th; a.tw = pl.tw; a.tiles_y = g.tiles_y; a.tiles_x = g.tiles_x;
     a.hw = g.hw; a.hp = g.hp; a.hpb = g.hpb;
-    a.cin16 = g.cin16; a.xs = g.xs; a.wsx = g.wsx;
+    a.cin16 = g.cin16; a.xs = g.xs;
     a.nchunk = g.nchunk; a.cpw = g.cpw; a.S = g.S;
     a.J = g.J; a.coj = g.coj; a.ob = g.ob; a.pb = g.pb;
-    a.o_x = g.o_x; a.o_w = g.o_w; a.o_be = g.o_be; a.o_wd = g.o_wd; a.o_bd = g.o_bd;
-    a.o_e = g.o_e; a.o_d = g.o_d; a.o_wp = g.o_wp; a.o_hv = g.o_hv; a.o_flag = g.o_flag;
     auto magic = [](int d) { return (unsigned)((0x100000000ull + (uint64_t)d - 1) / (uint64_t)d); };
     a.m_cin4 = magic(sh.cin / 4);
     a.m_c4n = magic(g.cin16 / 4);
@@ -750,16 +782,7 @@ int launch_ir(const shp::Launch& l) {
     a.m_J = magic(g.J);
     a.m_tx = magic(g.tiles_x);
     a.m_ty = magic(g.tiles_y);
-    int o = 0;
-    if (sh.expand) {
-        a.w_we = 0;
-        a.w_be = sh.ce * sh.cin;
-        o = a.w_be + sh.ce;
-    }
-    a.w_wd = o;
-    a.w_bd = a.w_wd + sh.k * sh.k * sh.ce;
-    a.w_wp = a.w_bd + sh.ce;
-    a.w_bp = a.w_wp + sh.cout * sh.ce;
+    a.w_wd = sh.expand ? sh.ce * (sh.cin + 1) : 0;
     const unsigned grid = (unsigned)((int64_t)g.tiles * g.J * g.S);
     const size_t lds = (size_t)g.lds_floats * sizeof(float);
     if (sh.k == 3)
