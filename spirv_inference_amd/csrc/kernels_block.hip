@@ -90,13 +90,22 @@ struct IrArgs {
     int J, coj, ob, pb;            // output-channel splits, channels per split (16 * ob),
                                    // 16-row blocks of the output tile
     int w_wd;  // packed-weight offset of the depthwise taps (ce * (cin + 1) with expand, else 0)
-    // ceil(2^32 / d) for the divisors cin / 4, cin16 / 4, hw, tw, S, J, tiles_x and tiles_y:
-    // n / d = umulhi(n, m) exactly for n * d < 2^32
+    // floor((2^32 - 1) / d) for the divisors cin / 4, cin16 / 4, hw, tw, S, J, tiles_x and
+    // tiles_y: n / d = umulhi(n + 1, m) exactly for (n + 1) * d <= 2^32, d = 1 included
     unsigned m_cin4, m_c4n, m_hw, m_tw, m_S, m_J, m_tx, m_ty;
 };
 
+// 16-byte buffer load; a byte offset at or past the range (kOob) reads zeros without a
+// memory access, so masked loads need no branch.
+constexpr unsigned kOob = 0x80000000u;
+__device__ __forceinline__ f4v ld16(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// One add and one multiply-high, no select on the divisor (a select split the kernel-argument
+// loads into three dependent scalar-load round trips).
 __device__ __forceinline__ int udiv(int n, unsigned m) {
-    return m ? (int)__umulhi((unsigned)n, m) : n;  // m = 0 stands for d = 1
+    return (int)__umulhi((unsigned)n + 1u, m);
 }
 
 // The idx-th float4 of one chunk's weights: the We rows (cin wide), then rows of 32 channels
@@ -131,15 +140,13 @@ __device__ __forceinline__ void weight_slot(const IrArgs& a, const IrLds& L, int
 // second half of a 16-channel last chunk) read as zeros.
 template <int U>
 __device__ __forceinline__ void fetch_weights(f4v (&pf)[NPF], const IrArgs& a,
-                                              const int (&goff)[NPF], const int (&meta)[NPF],
-                                              int tid, int nf, int ch) {
+                                              __amdgpu_buffer_rsrc_t wr, const int (&goff)[NPF],
+                                              const int (&meta)[NPF], int tid, int nf, int ch) {
     if constexpr (U < NPF) {
-        pf[U] = f4v{0.f, 0.f, 0.f, 0.f};
-        if (tid + 256 * U < nf && ch * CC + ((meta[U] >> 16) & 255) < a.ce) {
-            const int stp = (meta[U] >> 24) ? CC * a.cin : CC;
-            pf[U] = *reinterpret_cast<const f4v*>(a.w + goff[U] + stp * ch);
-        }
-        fetch_weights<U + 1>(pf, a, goff, meta, tid, nf, ch);
+        const bool ok = (tid + 256 * U < nf) & (ch * CC + ((meta[U] >> 16) & 255) < a.ce);
+        const int stp = (meta[U] >> 24) ? CC * a.cin : CC;
+        pf[U] = ld16(wr, ok ? (unsigned)(goff[U] + stp * ch) * 4u : kOob);
+        fetch_weights<U + 1>(pf, a, wr, goff, meta, tid, nf, ch);
     }
 }
 template <int U>
@@ -209,23 +216,20 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     const int xtotal = hrows * c4n;
     f4v xv[8];
     int xd[8];
+    // (branch-free: a float4 outside the image is a buffer load past the range, so zeros)
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x + (int64_t)img * a.h * a.w_ * a.cin,
+                                                  (int64_t)a.h * a.w_ * a.cin);
     auto load_x = [&](int e0) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int e = e0 + 256 * t;
-            xv[t] = f4v{0.f, 0.f, 0.f, 0.f};
-            xd[t] = -1;
-            if (e < xtotal) {
-                const int r = udiv(e, a.m_c4n), q = e - r * c4n;
-                xd[t] = r * a.xs + 4 * q;
-                if (r < a.hp && 4 * q < a.cin) {
-                    const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
-                    const int iy = iy0 + hy, ix = ix0 + hx;
-                    if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_)
-                        xv[t] = *reinterpret_cast<const f4v*>(
-                            a.x + (((int64_t)img * a.h + iy) * a.w_ + ix) * a.cin + 4 * q);
-                }
-            }
+            const int r = udiv(e, a.m_c4n), q = e - r * c4n;
+            const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+            const int iy = iy0 + hy, ix = ix0 + hx;
+            const bool in = (e < xtotal) & (r < a.hp) & (4 * q < a.cin) &
+                            ((unsigned)iy < (unsigned)a.h) & ((unsigned)ix < (unsigned)a.w_);
+            xv[t] = ld16(xr, in ? (unsigned)((iy * a.w_ + ix) * a.cin + 4 * q) * 4u : kOob);
+            xd[t] = e < xtotal ? r * a.xs + 4 * q : -1;
         }
     };
     auto store_x = [&]() {
@@ -243,7 +247,9 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         if (tid + 256 * u < nf) weight_slot<K>(a, L, j, tid + 256 * u, goff[u], meta[u]);
     }
     f4v pf[NPF];  // (native vectors: HIP's float4 struct copies would pin them to scratch)
-    fetch_weights<0>(pf, a, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
+    const __amdgpu_buffer_rsrc_t wr =
+        buffer_rsrc(a.w, a.w_wd + (int64_t)(K * K + 1 + a.cout) * a.ce + a.cout);
+    fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
 
     store_x();
     for (int e0 = tid + 2048; e0 < xtotal; e0 += 2048) {  // patches of more than 2048 float4
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         __syncthreads();  // the previous chunk's readers are done with its weights, E and D
         put_weights<0>(pf, lds, meta, tid, nf);
         if (ch + 1 < c_end)  // the next chunk's weights load while this one computes
-            fetch_weights<0>(pf, a, goff, meta, tid, nf, ch + 1);
+            fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, ch + 1);
         __syncthreads();
         const int c0 = ch * CC;
         const bool half = c0 + 16 >= a.ce;  // a 16-channel last chunk: one column block
@@ -292,6 +298,10 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
                 const bool two = hb + 4 < a.hpb;
                 const float* xa0 = Xs + (hb * 16 + li) * a.xs + g * Q;
                 const float* xa1 = two ? xa0 + 64 * a.xs : xa0;
+                // validity of this lane's 4 accumulator rows (one 16-byte read each, issued
+                // ahead of the products instead of one dependent read per row after them)
+                const int4 in0 = *reinterpret_cast<const int4*>(hvalid + hb * 16 + 4 * g);
+                const int4 in1 = *reinterpret_cast<const int4*>(hvalid + (two ? hb + 4 : hb) * 16 + 4 * g);
                 floatx4 e00 = {0.f, 0.f, 0.f, 0.f}, e01 = e00, e10 = e00, e11 = e00;
                 f4v x0 = *reinterpret_cast<const f4v*>(xa0);
                 f4v x1 = *reinterpret_cast<const f4v*>(xa1);
@@ -320,13 +330,13 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {  // accumulator r: row 4g + r, column li
                     const int row = hb * 16 + 4 * g + r;
-                    const bool in = hvalid[row];
+                    const bool in = (&in0.x)[r];
                     Es[row * ES + li] = in ? act_e(e00[r] + be0) : 0.f;
                     Es[row * ES + 16 + li] = in && !half ? act_e(e01[r] + be1) : 0.f;
                     if (two) {
-                        const bool in1 = hvalid[row + 64];
-                        Es[(row + 64) * ES + li] = in1 ? act_e(e10[r] + be0) : 0.f;
-                        Es[(row + 64) * ES + 16 + li] = in1 && !half ? act_e(e11[r] + be1) : 0.f;
+                        const bool in1r = (&in1.x)[r];
+                        Es[(row + 64) * ES + li] = in1r ? act_e(e10[r] + be0) : 0.f;
+                        Es[(row + 64) * ES + 16 + li] = in1r && !half ? act_e(e11[r] + be1) : 0.f;
                     }
                 }
             }
@@ -387,30 +397,44 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         }
     }
 
-    auto store = [&](int b, int l, floatx4 v) {  // bias, residual, activation of 4 outputs
+    // Output position (projection block b, lane l): 4 pixels of one output channel.  Its
+    // bias and residuals load first (pre), ahead of the split sums, and the sums then store
+    // with them (store); idx < 0 marks pixels outside the map.
+    struct Out {
+        int64_t idx[4];
+        float bias;
+        f4v res;
+    };
+    auto pre = [&](int b, int l) {
+        Out u;
         const int pbi = b / a.ob, obi = b - pbi * a.ob;
         const int oo = obi * 16 + (l & 15);
-        if (oo >= cv) return;
         const int o = j * a.coj + oo;
-        const float bias = a.w[a.w_wd + (K * K + 1 + a.cout) * a.ce + o];
+        u.bias = 0.f;
+        u.res = f4v{0.f, 0.f, 0.f, 0.f};
+        if (oo < cv) u.bias = a.w[a.w_wd + (K * K + 1 + a.cout) * a.ce + o];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int p = pbi * 16 + 4 * (l >> 4) + r;
-            if (p >= P) continue;
             const int py = udiv(p, a.m_tw), px = p - py * a.tw;
             const int oy = oy0 + py, ox = ox0 + px;
-            if (oy >= a.oh || ox >= a.ow) continue;
-            const int64_t idx = (((int64_t)img * a.oh + oy) * a.ow + ox) * a.cout + o;
-            float vv = v[r] + bias;
-            if (a.res) vv += a.res[idx];
-            a.y[idx] = shpd::apply_act(vv, a.act_o, a.alpha);
+            const bool ok = oo < cv && p < P && oy < a.oh && ox < a.ow;
+            u.idx[r] = ok ? (((int64_t)img * a.oh + oy) * a.ow + ox) * a.cout + o : -1;
+            if (ok && a.res) u.res[r] = a.res[u.idx[r]];
         }
+        return u;
+    };
+    auto store = [&](const Out& u, floatx4 v) {  // bias, residual, activation of 4 outputs
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (u.idx[r] >= 0)
+                a.y[u.idx[r]] = shpd::apply_act(v[r] + u.bias + u.res[r], a.act_o, a.alpha);
     };
 
     if (a.S == 1) {
 #pragma unroll
         for (int i = 0; i < NBW; ++i)
-            if (wave + 4 * i < nblk) store(wave + 4 * i, lane, acc[i]);
+            if (wave + 4 * i < nblk) store(pre(wave + 4 * i, lane), acc[i]);
         return;
     }
     // split expanded channels: partials, then the last arrival sums them
@@ -439,9 +463,16 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     // tile fits one pass, else 2 positions x 8 splits
     if (W <= 256) {
         if (tid < W) {
+            float4 q[16];
             f4v t = f4v{0.f, 0.f, 0.f, 0.f};
-            for (int s0 = 0; s0 < a.S; s0 += 16) {
-                float4 q[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (u < a.S) q[u] = ld_coh16(prs, (unsigned)((u * W + tid) * 16), 0);
+            const Out op = pre(tid >> 6, tid & 63);  // its loads go out behind the partials
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (u < a.S) t += f4v{q[u].x, q[u].y, q[u].z, q[u].w};
+            for (int s0 = 16; s0 < a.S; s0 += 16) {
 #pragma unroll
                 for (int u = 0; u < 16; ++u)
                     if (s0 + u < a.S)
@@ -450,21 +481,28 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
                 for (int u = 0; u < 16; ++u)
                     if (s0 + u < a.S) t += f4v{q[u].x, q[u].y, q[u].z, q[u].w};
             }
-            store(tid >> 6, tid & 63, floatx4{t.x, t.y, t.z, t.w});
+            store(op, floatx4{t.x, t.y, t.z, t.w});
         }
     } else
     for (int f0 = tid; f0 < W; f0 += 512) {
+        float4 q[2][8];
         f4v t[2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m) t[m] = f4v{0.f, 0.f, 0.f, 0.f};
+        Out op[2];
         for (int s0 = 0; s0 < a.S; s0 += 8) {
-            float4 q[2][8];
 #pragma unroll
             for (int m = 0; m < 2; ++m)
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
                     if (f0 + 256 * m < W && s0 + u < a.S)
                         q[m][u] = ld_coh16(prs, (unsigned)(((s0 + u) * W + f0 + 256 * m) * 16), 0);
+            if (s0 == 0) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int f = min(f0 + 256 * m, W - 1);
+                    op[m] = pre(f >> 6, f & 63);
+                    t[m] = f4v{0.f, 0.f, 0.f, 0.f};
+                }
+            }
 #pragma unroll
             for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -475,7 +513,7 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             const int f = f0 + 256 * m;
-            if (f < W) store(f >> 6, f & 63, floatx4{t[m].x, t[m].y, t[m].z, t[m].w});
+            if (f < W) store(op[m], floatx4{t[m].x, t[m].y, t[m].z, t[m].w});
         }
     }
     if (tid == 0)
@@ -536,7 +574,7 @@ bool geometry_ok(const IrGeom& g) {
            (int64_t)g.S * g.nblk * 1024 < (1ll << 31) &&
            // the kernel's multiply-high divisions of the workgroup id stay exact
            (int64_t)g.tiles * g.J * g.S *
-                   std::max(std::max(g.S, g.J), std::max(g.tiles_x, g.tiles_y)) < (1ll << 32) &&
+                   std::max(std::max(g.S, g.J), std::max(g.tiles_x, g.tiles_y)) < (1ll << 31) &&
            (g.S == 1 || (int64_t)g.tiles * g.J <= (int64_t)(shp::kSplitCounterBytes / sizeof(int))) &&
            (int64_t)g.tiles * g.J * g.S < (1ll << 31);
 }
@@ -710,7 +748,10 @@ int parse(const int32_t* q, size_t n, IrShape& sh) {
         return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: total != n*oh*ow*cout");
     const int64_t wn = (sh.expand ? (int64_t)sh.ce * sh.cin + sh.ce : 0) +
                        (int64_t)sh.k * sh.k * sh.ce + sh.ce + (int64_t)sh.cout * sh.ce + sh.cout;
-    if (wn >= (1ll << 31) || (int64_t)sh.n * sh.h * sh.w * sh.cin >= (1ll << 40))
+    // the halo and weight loads are buffer loads with 32-bit byte offsets over one image of x
+    // and over the packed weights
+    if (wn * 4 >= (1ll << 31) || (int64_t)sh.h * sh.w * sh.cin * 4 >= (1ll << 31) ||
+        (int64_t)sh.n * sh.h * sh.w * sh.cin >= (1ll << 40))
         return shp::fail(SHP_ERR_SHAPE, "inverted_residual_nhwc: tensors too large");
     return SHP_OK;
 }
@@ -773,7 +814,7 @@ int launch_ir(const shp::Launch& l) {
     a.cin16 = g.cin16; a.xs = g.xs;
     a.nchunk = g.nchunk; a.cpw = g.cpw; a.S = g.S;
     a.J = g.J; a.coj = g.coj; a.ob = g.ob; a.pb = g.pb;
-    auto magic = [](int d) { return (unsigned)((0x100000000ull + (uint64_t)d - 1) / (uint64_t)d); };
+    auto magic = [](int d) { return (unsigned)(0xFFFFFFFFull / (uint64_t)d); };
     a.m_cin4 = magic(sh.cin / 4);
     a.m_c4n = magic(g.cin16 / 4);
     a.m_hw = magic(g.hw);
