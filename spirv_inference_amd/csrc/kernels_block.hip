@@ -308,13 +308,11 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
                 f4v b0 = *reinterpret_cast<const f4v*>(wb0);
                 f4v b1 = *reinterpret_cast<const f4v*>(wb1);
                 for (int u = 4; u <= Q; u += 4) {
-                    f4v nx0 = x0, nx1 = x1, nb0 = b0, nb1 = b1;
-                    if (u < Q) {
-                        nx0 = *reinterpret_cast<const f4v*>(xa0 + u);
-                        nx1 = *reinterpret_cast<const f4v*>(xa1 + u);
-                        nb0 = *reinterpret_cast<const f4v*>(wb0 + u);
-                        nb1 = *reinterpret_cast<const f4v*>(wb1 + u);
-                    }
+                    // (at u = Q the reads land in the rows' padding, 4 Q = cin16 < xs, unused)
+                    const f4v nx0 = *reinterpret_cast<const f4v*>(xa0 + u);
+                    const f4v nx1 = *reinterpret_cast<const f4v*>(xa1 + u);
+                    const f4v nb0 = *reinterpret_cast<const f4v*>(wb0 + u);
+                    const f4v nb1 = *reinterpret_cast<const f4v*>(wb1 + u);
                     // zero weights past ce (a 16-channel last chunk) in the second column block
                     e00 = mfma4(x0, b0, e00);
                     e01 = mfma4(x0, b1, e01);
