@@ -44,6 +44,9 @@ struct GemmTune {
     // to pay (0), always (1), or as the three operators the TFLite scheduler dispatches (-1);
     // read when a model is built
     int ir_fuse = 0;
+    // conv2d_nhwc with <= 4 input channels: the direct kernel where it fits (0) or the
+    // implicit-GEMM kernels (-1)
+    int conv_direct = 0;
 };
 
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.
@@ -102,6 +105,9 @@ size_t block_workspace_for_kernel(const int32_t* push, size_t n_push, const Gemm
 // Whether that kernel takes this push vector and is expected to beat the block's three
 // operators (measured verdicts for the benchmark configs' blocks, a rule elsewhere).
 bool block_fusion_pays(const int32_t* push, size_t n_push);
+// conv2d_nhwc with at most 4 input channels (the 3-channel image stems) as a direct
+// convolution (kernels_spatial.hip): SHP_ERR_UNSUPPORTED when the shape does not fit it.
+int conv_nhwc_direct(const Launch& l);
 
 // Counter-based RNG fill (kernels_elementwise.hip).
 int fill_random(hipStream_t stream, float* p, uint64_t n, uint64_t seed, uint64_t tensor_id,

@@ -2236,6 +2236,10 @@ int conv2d_common(const shp::Launch& l, bool nhwc) {
     p.residual = l.epi->residual;
     p.act = l.epi->act;
     p.alpha = l.epi->alpha;
+    if (nhwc && q[1] <= 4 && !(l.tune && l.tune->conv_direct < 0)) {
+        rc = shp::conv_nhwc_direct(l);
+        if (rc != SHP_ERR_UNSUPPORTED) return rc;
+    }
     int bm = (p.K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
     if (nhwc) {
         int am = (p.cic % 4 == 0 && al16(p.a)) ? shp::A_CONV_NHWC4 : shp::A_CONV_NHWC;

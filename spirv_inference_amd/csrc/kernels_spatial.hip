@@ -11,6 +11,7 @@
 // each thread then produces four adjacent channels of two output pixels from LDS.  The taps
 // are summed in the reference loop order, skipping the padding taps.
 #include "common.h"
+#include "coherent.h"
 
 namespace {
 
@@ -466,9 +467,132 @@ int launch_resize_bilinear(const shp::Launch& l) {
     return SHP_OK;
 }
 
+// ---- conv2d_nhwc 3x3 with 1-4 input channels (the 3-channel image stems) ------------------
+// An implicit GEMM would run K = KH*KW*CI (27 for a 3x3 stem) through tiles built for deep K.
+// Here one thread makes 8 adjacent output channels of one pixel: it loads the pixel's
+// KH*KW*CI input values once (buffer loads; taps in the padding read zeros), then sums them
+// against the workgroup's weights, staged in LDS as [k][oc] so the 8 weights of one tap are
+// two 16-byte reads that every thread of a pixel group shares.  Sums start at the bias and
+// run channel, kernel row, kernel column, as the reference loops (scheduler.rs:321-427).
+struct ConvD {
+    int h, w, oc, oh, ow, kh, kw, sh, sw, pt, pl, ocg, total;
+    unsigned m_ocg, m_ow, m_oh;  // floor((2^32 - 1) / d): n / d = umulhi(n + 1, m)
+};
+
+__device__ __forceinline__ int udiv_mh(int n, unsigned m) {
+    return (int)__umulhi((unsigned)n + 1u, m);
+}
+
+template <int CI, int KH, int KW>
+__global__ __launch_bounds__(256) void conv_direct_nhwc_kernel(const float* __restrict__ x,
+                                                               const float* __restrict__ w,
+                                                               float* __restrict__ y, ConvD d,
+                                                               const float* __restrict__ res,
+                                                               int act, float alpha) {
+    extern __shared__ __attribute__((aligned(16))) float cw[];  // [K][oc] weights, oc biases
+    constexpr int KK = KH * KW;
+    constexpr int K = KK * CI;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < K * d.oc; e += 256) {  // OHWI -> [k][oc]
+        const int o = e / K, k = e - o * K;
+        cw[k * d.oc + o] = w[e];
+    }
+    for (int e = tid; e < d.oc; e += 256) cw[K * d.oc + e] = w[K * d.oc + e];
+    __syncthreads();
+    const int idx = blockIdx.x * 256 + tid;
+    if (idx >= d.total) return;
+    const int pix = udiv_mh(idx, d.m_ocg), g = idx - pix * d.ocg;
+    const int q = udiv_mh(pix, d.m_ow), ox = pix - q * d.ow;
+    const int img = udiv_mh(q, d.m_oh), oy = q - img * d.oh;
+    const int iy0 = oy * d.sh - d.pt, ix0 = ox * d.sw - d.pl;
+    const __amdgpu_buffer_rsrc_t xr =
+        buffer_rsrc(x + (int64_t)img * d.h * d.w * CI, (int64_t)d.h * d.w * CI);
+    float v[K];
+#pragma unroll
+    for (int t = 0; t < KK; ++t) {
+        const int ky = t / KW, kx = t % KW;
+        const int iy = iy0 + ky, ix = ix0 + kx;
+        const bool ok = ((unsigned)iy < (unsigned)d.h) & ((unsigned)ix < (unsigned)d.w);
+        const unsigned off = ok ? (unsigned)((iy * d.w + ix) * CI) * 4u : 0x80000000u;
+#pragma unroll
+        for (int c = 0; c < CI; ++c)
+            v[t * CI + c] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(xr, off + 4u * c, 0u, 0));
+    }
+    const float* wg = cw + 8 * g;
+    f4v a0 = *reinterpret_cast<const f4v*>(wg + K * d.oc);
+    f4v a1 = *reinterpret_cast<const f4v*>(wg + K * d.oc + 4);
+#pragma unroll
+    for (int c = 0; c < CI; ++c) {
+#pragma unroll
+        for (int t = 0; t < KK; ++t) {
+            const float* wk = wg + (t * CI + c) * d.oc;
+            const f4v w0 = *reinterpret_cast<const f4v*>(wk);
+            const f4v w1 = *reinterpret_cast<const f4v*>(wk + 4);
+            const float xv = v[t * CI + c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a0[j] = fmaf(xv, w0[j], a0[j]);
+                a1[j] = fmaf(xv, w1[j], a1[j]);
+            }
+        }
+    }
+    const int64_t o = (int64_t)pix * d.oc + 8 * g;
+    if (res) {
+        a0 += *reinterpret_cast<const f4v*>(res + o);
+        a1 += *reinterpret_cast<const f4v*>(res + o + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a0[j] = shpd::apply_act(a0[j], act, alpha);
+        a1[j] = shpd::apply_act(a1[j], act, alpha);
+    }
+    *reinterpret_cast<f4v*>(y + o) = a0;
+    *reinterpret_cast<f4v*>(y + o + 4) = a1;
+}
+
 }  // namespace
 
 namespace shp {
+
+int conv_nhwc_direct(const Launch& l) {
+    // push {n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, same, pt, pl, total}, checked by the
+    // caller (positive dims, total)
+    const int32_t* q = l.push;
+    const int n = q[0], ci = q[1], oc = q[4], kh = q[7], kw = q[8];
+    const int64_t K = (int64_t)kh * kw * ci;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (ci > 4 || kh != 3 || kw != 3 || oc % 8 || (K + 1) * oc * 4 > 65536 || !al16(l.out) ||
+        (l.epi->residual && !al16(l.epi->residual)))
+        return SHP_ERR_UNSUPPORTED;
+    ConvD d;
+    d.h = q[2]; d.w = q[3]; d.oc = oc; d.oh = q[5]; d.ow = q[6]; d.kh = kh; d.kw = kw;
+    d.sh = q[9]; d.sw = q[10]; d.pt = q[12]; d.pl = q[13]; d.ocg = oc / 8;
+    const int64_t total = (int64_t)n * d.oh * d.ow * d.ocg;
+    const int64_t dmax = std::max<int64_t>(d.ocg, std::max(d.ow, d.oh));
+    // one image's input within the buffer loads' 32-bit byte offsets; the multiply-high
+    // divisions exact for every thread index
+    if ((int64_t)d.h * d.w * ci * 4 >= (1ll << 31) || (total + 1) * dmax > (1ll << 32))
+        return SHP_ERR_UNSUPPORTED;
+    d.total = (int)total;
+    d.m_ocg = (unsigned)(0xFFFFFFFFull / (uint64_t)d.ocg);
+    d.m_ow = (unsigned)(0xFFFFFFFFull / (uint64_t)d.ow);
+    d.m_oh = (unsigned)(0xFFFFFFFFull / (uint64_t)d.oh);
+    const dim3 grid(grid_1d((uint64_t)total, 256));
+    const size_t lds = (size_t)(K + 1) * oc * 4;
+    const float* x = (const float*)l.in0;
+    const float* w = (const float*)l.in1;
+    float* y = (float*)l.out;
+    const float* res = l.epi->residual;
+    switch (ci) {
+        case 1: hipLaunchKernelGGL((conv_direct_nhwc_kernel<1, 3, 3>), grid, dim3(256), lds, l.stream, x, w, y, d, res, l.epi->act, l.epi->alpha); break;
+        case 2: hipLaunchKernelGGL((conv_direct_nhwc_kernel<2, 3, 3>), grid, dim3(256), lds, l.stream, x, w, y, d, res, l.epi->act, l.epi->alpha); break;
+        case 3: hipLaunchKernelGGL((conv_direct_nhwc_kernel<3, 3, 3>), grid, dim3(256), lds, l.stream, x, w, y, d, res, l.epi->act, l.epi->alpha); break;
+        default: hipLaunchKernelGGL((conv_direct_nhwc_kernel<4, 3, 3>), grid, dim3(256), lds, l.stream, x, w, y, d, res, l.epi->act, l.epi->alpha); break;
+    }
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
 
 KernelEntry kSpatialKernels[] = {
     {"depthwise_conv2d", 16, true, launch_dw_nchw},

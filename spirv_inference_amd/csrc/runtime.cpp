@@ -344,6 +344,7 @@ int shp_tune(shp_ctx* ctx, const char* key, int value) {
     else if (k == "ir_splits") t.ir_s = value;
     else if (k == "ir_cout_splits") t.ir_j = value;
     else if (k == "ir_fuse") t.ir_fuse = value;
+    else if (k == "conv_direct") t.conv_direct = value;
     else return fail(SHP_ERR_INVALID, "shp_tune: unknown key '" + k + "'");
     return SHP_OK;
 }

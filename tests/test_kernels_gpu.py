@@ -664,6 +664,43 @@ def test_conv2d_reference_and_nhwc(ctx, orc, n, ic, hw, oc, k, s, pad):
     assert_close(y, r, 1e-4, 1e-4, "conv2d nhwc")
 
 
+@pytest.mark.parametrize("n,ic,h,w,oc,s,act,res", [
+    (1, 3, 224, 224, 32, 2, "relu6", False),   # MobileNetV2 / EfficientNet-Lite0 stem
+    (8, 3, 224, 224, 32, 2, "relu6", False),
+    (2, 1, 17, 13, 16, 1, "relu", True),
+    (3, 4, 9, 11, 8, 2, None, False),
+    (2, 2, 10, 7, 24, 1, "relu6", True)],
+    ids=["stem-b1", "stem-b8", "ic1-res", "ic4-odd", "ic2-res"])
+def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, res):
+    """3x3 conv2d_nhwc with 1-4 input channels (SAME padding) runs the direct kernel (one
+    thread: 8 output channels of one pixel, taps in the padding read as zeros): against the
+    oracle, and against the implicit-GEMM kernels with the direct kernel switched off (both
+    agree with the oracle; the two sum in different orders, so some outputs differ in the
+    last bits, which shows the direct kernel ran)."""
+    k = 3
+    oh, ow = (h + s - 1) // s, (w + s - 1) // s
+    pt = max((oh - 1) * s + k - h, 0) // 2
+    pl = max((ow - 1) * s + k - w, 0) // 2
+    total = n * oh * ow * oc
+    push = [n, ic, h, w, oc, oh, ow, k, k, s, s, 1, pt, pl, total]
+    wt = np.concatenate([rnd(oc * k * k * ic, scale=float(np.sqrt(2.0 / (k * k * ic)))),
+                         rnd(oc, scale=0.1)])
+    x = rnd(n, h, w, ic)
+    kw = {"act": act} if act else {}
+    if res:
+        kw["residual"] = rnd(total)
+    y, r = both(ctx, orc, "conv2d_nhwc", x, wt, total, push, **kw)
+    assert_close(y, r, 1e-4, 1e-4, f"direct conv {push[:14]}")
+    try:
+        _tune(ctx, "conv_direct", -1)
+        y0 = hip(ctx, "conv2d_nhwc", x, wt, total, push, **kw)
+    finally:
+        _tune(ctx, "conv_direct", 0)
+    assert_close(y0, r, 1e-4, 1e-4, f"implicit-GEMM conv {push[:14]}")
+    if n * oh * ow >= 1000:
+        assert not np.array_equal(y, y0), "the direct kernel did not run"
+
+
 @pytest.mark.parametrize("b,k,n", [(1, 1280, 1000), (8, 1280, 1000), (32, 2048, 1000),
                                    (3, 37, 5)])
 def test_fully_connected(ctx, orc, b, k, n):
