@@ -604,42 +604,43 @@ double plan_cost(const IrShape& sh, const IrGeom& g) {
 }
 
 // Plans measured best on MI355X for the MBConv blocks of the benchmark configs (every tile,
-// split and output-channel slice per block, each timed as 20 launches replayed from a
-// hipGraph), and whether one launch beat the three operators (conv2d_nhwc,
-// depthwise_conv2d_nhwc, conv2d_nhwc) in the whole model's graph replay.  The cost model and
-// the rule of fusion_pays cover every other shape.
+// split and output-channel slice per block, each timed as 20 launches of the block replayed
+// from a hipGraph, beside the three operators conv2d_nhwc, depthwise_conv2d_nhwc, conv2d_nhwc
+// timed the same way), and whether one launch beat the three operators; where the two were
+// close the whole model's graph replay decided.  The cost model and the rule of fusion_pays
+// cover every other shape.
 struct TunedBlock {
     int n, cin, h, w, ce, cout, k, s, expand;
     int th, tw, S, J;
     bool fuse;
 };
 const TunedBlock kTunedBlocks[] = {
-    // MobileNetV2-1.0 batch 1 (us in the model's graph replay: one launch / three launches)
-    {1, 32, 112, 112, 32, 16, 3, 1, 0, 7, 7, 1, 1, true},     // block0: 10.2 / 10.4
-    {1, 16, 112, 112, 96, 24, 3, 2, 1, 8, 2, 1, 1, true},     // block1: 16.3 / 18.3
-    {1, 24, 56, 56, 144, 24, 3, 1, 1, 8, 4, 4, 1, true},      // block2: 15.9 / 23.5
-    {1, 24, 56, 56, 144, 32, 3, 2, 1, 8, 2, 3, 1, true},      // block3: 16.4 / 20.1
-    {1, 32, 28, 28, 192, 32, 3, 1, 1, 8, 4, 6, 1, true},      // block4-5: 12.3 / 21.6-27.4
-    {1, 32, 28, 28, 192, 64, 3, 2, 1, 4, 2, 6, 1, true},      // block6: 12.3 / 20.0
-    {1, 64, 14, 14, 384, 64, 3, 1, 1, 8, 2, 12, 2, true},     // block7-9: 14.4-15.0 / 21.3-23.2
-    {1, 64, 14, 14, 384, 96, 3, 1, 1, 8, 2, 12, 2, true},     // block10: 14.2 / 21.2
-    {1, 96, 14, 14, 576, 96, 3, 1, 1, 7, 2, 16, 2, true},     // block11-12: 17.5 / 22.4-23.0
-    {1, 96, 14, 14, 576, 160, 3, 2, 1, 7, 1, 12, 4, true},    // block13: 17.7 / 23.0
-    {1, 160, 7, 7, 960, 160, 3, 1, 1, 7, 2, 16, 3, true},     // block14-15: 21.1 / 24.6
-    {1, 160, 7, 7, 960, 320, 3, 1, 1, 7, 2, 16, 4, true},     // block16: 23.2 / 25.4
+    // MobileNetV2-1.0 batch 1 (us per launch: one launch / three launches)
+    {1, 32, 112, 112, 32, 16, 3, 1, 0, 7, 7, 1, 1, true},     // block0: 7.4 / 10.3
+    {1, 16, 112, 112, 96, 24, 3, 2, 1, 8, 4, 3, 1, true},     // block1: 11.9 / 19.6
+    {1, 24, 56, 56, 144, 24, 3, 1, 1, 8, 4, 4, 1, true},      // block2: 13.4 / 20.4
+    {1, 24, 56, 56, 144, 32, 3, 2, 1, 4, 2, 3, 1, true},      // block3: 12.7 / 18.8
+    {1, 32, 28, 28, 192, 32, 3, 1, 1, 8, 4, 6, 1, true},      // block4-5: 10.5 / 18.6
+    {1, 32, 28, 28, 192, 64, 3, 2, 1, 7, 1, 6, 1, true},      // block6: 10.3 / 17.9
+    {1, 64, 14, 14, 384, 64, 3, 1, 1, 8, 2, 12, 1, true},     // block7-9: 11.7 / 18.5
+    {1, 64, 14, 14, 384, 96, 3, 1, 1, 8, 4, 12, 4, true},     // block10: 12.2 / 18.0
+    {1, 96, 14, 14, 576, 96, 3, 1, 1, 8, 2, 16, 2, true},     // block11-12: 14.6 / 19.9
+    {1, 96, 14, 14, 576, 160, 3, 2, 1, 7, 1, 16, 4, true},    // block13: 14.6 / 19.9
+    {1, 160, 7, 7, 960, 160, 3, 1, 1, 4, 4, 16, 3, true},     // block14-15: 16.8 / 21.7
+    {1, 160, 7, 7, 960, 320, 3, 1, 1, 7, 2, 16, 3, true},     // block16: 18.8 / 21.9
     // EfficientNet-Lite0 batch 8
-    {8, 32, 112, 112, 32, 16, 3, 1, 0, 8, 7, 1, 1, false},    // block0: 32.0 / 25.1
-    {8, 16, 112, 112, 96, 24, 3, 2, 1, 7, 4, 1, 1, true},     // block1: 39.3 / 43.4
-    {8, 24, 56, 56, 144, 24, 3, 1, 1, 7, 7, 1, 1, true},      // block2: 30.0 / 41.2
-    {8, 24, 56, 56, 144, 40, 5, 2, 1, 7, 2, 1, 1, true},      // block3: 30.3 / 36.7
-    {8, 40, 28, 28, 240, 40, 5, 1, 1, 7, 7, 2, 1, true},      // block4: 32.6 / 38.4
-    {8, 40, 28, 28, 240, 80, 3, 2, 1, 7, 2, 4, 1, false},     // block5: 32.4 / 29.3
-    {8, 80, 14, 14, 480, 80, 3, 1, 1, 8, 4, 8, 1, false},     // block6-7: 26.8-28.1 / 24.9-25.1
-    {8, 80, 14, 14, 480, 112, 5, 1, 1, 4, 4, 4, 1, false},    // block8: 32.0 / 30.2
-    {8, 112, 14, 14, 672, 112, 5, 1, 1, 4, 4, 4, 1, false},   // block9-10: 44.3 / 35.7 (alone)
-    {8, 112, 14, 14, 672, 192, 5, 2, 1, 7, 2, 8, 1, false},   // block11: 33.4 / 29.0 (alone)
-    {8, 192, 7, 7, 1152, 192, 5, 1, 1, 7, 4, 8, 2, false},    // block12-14: 53.6 / 29.8 (alone)
-    {8, 192, 7, 7, 1152, 320, 3, 1, 1, 7, 4, 8, 2, false},    // block15: 57.2 / 27.7 (alone)
+    {8, 32, 112, 112, 32, 16, 3, 1, 0, 8, 7, 1, 1, true},     // block0: 24.6 / 29.5
+    {8, 16, 112, 112, 96, 24, 3, 2, 1, 7, 4, 1, 1, true},     // block1: 32.5 / 42.7
+    {8, 24, 56, 56, 144, 24, 3, 1, 1, 8, 7, 1, 1, true},      // block2: 27.2 / 43.5
+    {8, 24, 56, 56, 144, 40, 5, 2, 1, 7, 2, 1, 1, true},      // block3: 24.6 / 41.6
+    {8, 40, 28, 28, 240, 40, 5, 1, 1, 7, 7, 4, 1, true},      // block4: 23.6 / 40.1
+    {8, 40, 28, 28, 240, 80, 3, 2, 1, 8, 2, 4, 1, true},      // block5: 17.4 / 27.5
+    {8, 80, 14, 14, 480, 80, 3, 1, 1, 7, 4, 8, 1, true},      // block6-7: 22.6 / 25.6
+    {8, 80, 14, 14, 480, 112, 5, 1, 1, 4, 4, 4, 1, true},     // block8: 26.3 / 29.5
+    {8, 112, 14, 14, 672, 112, 5, 1, 1, 4, 4, 4, 1, false},   // block9-10: 38.5 / 36.5
+    {8, 112, 14, 14, 672, 192, 5, 2, 1, 7, 2, 8, 1, true},    // block11: 28.0 / 28.8
+    {8, 192, 7, 7, 1152, 192, 5, 1, 1, 7, 4, 8, 2, false},    // block12-14: 45.6 / 29.7
+    {8, 192, 7, 7, 1152, 320, 3, 1, 1, 7, 4, 8, 2, false},    // block15: 42.7 / 27.8
 };
 
 const TunedBlock* tuned_block(const IrShape& sh) {
