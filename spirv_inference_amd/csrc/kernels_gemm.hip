@@ -1495,6 +1495,63 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
     }
 }
 
+// The same product for 2..8 rows with the rows staged in LDS once per workgroup: each
+// wavefront takes two output columns, so the M activation rows are read from L2 once per
+// eight columns (the kernel above reads them once per column, 40 KB per column at M = 8,
+// K = 1280).  Per lane and column the sums run in the same order as in the kernel above.
+template <int MR>
+__global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ y, int M, int N,
+                                                            int K, const float* __restrict__ bias,
+                                                            int act, float alpha) {
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [M][K]
+    for (int i = threadIdx.x * 4; i < M * K; i += 1024)
+        *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int n0 = blockIdx.x * 8 + 2 * (threadIdx.x >> 6);
+    if (n0 >= N) return;
+    const bool two = n0 + 1 < N;
+    const float* w0 = w + (int64_t)n0 * K;
+    const float* w1 = two ? w0 + K : w0;
+    float a0[MR], a1[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) a0[m] = a1[m] = 0.0f;
+    for (int k = lane * 4; k < K; k += 256) {
+        const float4 u = *reinterpret_cast<const float4*>(w0 + k);
+        const float4 v = *reinterpret_cast<const float4*>(w1 + k);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m < M) {
+                const float4 xv = *reinterpret_cast<const float4*>(xs + m * K + k);
+                a0[m] += u.x * xv.x + u.y * xv.y + u.z * xv.z + u.w * xv.w;
+                a1[m] += v.x * xv.x + v.y * xv.y + v.z * xv.z + v.w * xv.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float p = a0[m], q = a1[m];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            p += __shfl_xor(p, o);
+            q += __shfl_xor(q, o);
+        }
+        a0[m] = p;
+        a1[m] = q;
+    }
+    if (lane == 0) {
+        const float b0 = bias ? bias[n0] : 0.0f;
+        for (int m = 0; m < M; ++m) y[(int64_t)m * N + n0] = shpd::apply_act(a0[m] + b0, act, alpha);
+        if (two) {
+            const float b1 = bias ? bias[n0 + 1] : 0.0f;
+            for (int m = 0; m < M; ++m)
+                y[(int64_t)m * N + n0 + 1] = shpd::apply_act(a1[m] + b1, act, alpha);
+        }
+    }
+}
+
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
     int bm, bn, bk;
@@ -2272,6 +2329,10 @@ int launch_fully_connected(const shp::Launch& l) {
             hipLaunchKernelGGL((skinny_nt_kernel<1>), dim3(g), dim3(256), 0, l.stream,
                                (const float*)l.in0, w, (float*)l.out, M, N, K, bias,
                                l.epi->act, l.epi->alpha);
+        else if (K % 4 == 0 && al16(l.in0) && al16(w) && (int64_t)M * K * 4 <= 65536)
+            hipLaunchKernelGGL((skinny_nt_lds_kernel<8>), dim3((unsigned)((N + 7) / 8)),
+                               dim3(256), (size_t)M * K * 4, l.stream, (const float*)l.in0, w,
+                               (float*)l.out, M, N, K, bias, l.epi->act, l.epi->alpha);
         else
             hipLaunchKernelGGL((skinny_nt_kernel<8>), dim3(g), dim3(256), 0, l.stream,
                                (const float*)l.in0, w, (float*)l.out, M, N, K, bias,

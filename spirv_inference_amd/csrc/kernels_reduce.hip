@@ -418,6 +418,39 @@ __global__ __launch_bounds__(1024) void softmax_whole_kernel(const float* __rest
     for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = expf(x[i] - m) / s;
 }
 
+// The same softmax for n <= 1024 * R in one pass over memory: each thread loads its R
+// elements at once and keeps them and their exponentials in registers.  The per-thread sums
+// run in the same element order and the reductions are the same, so the results equal the
+// three-pass kernel's bit for bit.
+template <int R>
+__global__ __launch_bounds__(1024) void softmax_whole_reg_kernel(const float* __restrict__ x,
+                                                                 float* __restrict__ y, int n) {
+    __shared__ float red[16];
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + r * 1024;
+        v[r] = i < n ? x[i] : kNegMax;
+    }
+    float m = kNegMax;
+#pragma unroll
+    for (int r = 0; r < R; ++r) m = fmaxf(m, v[r]);
+    m = block_max(m, red);
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + r * 1024;
+        v[r] = expf(v[r] - m);
+        if (i < n) s += v[r];
+    }
+    s = block_sum(s, red);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + r * 1024;
+        if (i < n) y[i] = v[r] / s;
+    }
+}
+
 int launch_softmax10(const shp::Launch& l) {
     if (l.out_elems != 10)
         return shp::fail(SHP_ERR_SHAPE, "softmax10: the reference kernel is fixed at 10 classes");
@@ -432,8 +465,17 @@ int launch_softmax1000(const shp::Launch& l) {
     int rc = shp::check_total(l, l.push[0], "softmax1000");
     if (rc) return rc;
     if (l.push[0] <= 0) return shp::fail(SHP_ERR_SHAPE, "softmax1000: class_count <= 0");
-    hipLaunchKernelGGL(softmax_whole_kernel, dim3(1), dim3(1024), 0, l.stream,
-                       (const float*)l.in0, (float*)l.out, l.push[0]);
+    const int n = l.push[0];
+    const float* x = (const float*)l.in0;
+    float* y = (float*)l.out;
+    if (n <= 1024)
+        hipLaunchKernelGGL((softmax_whole_reg_kernel<1>), dim3(1), dim3(1024), 0, l.stream, x, y, n);
+    else if (n <= 2048)
+        hipLaunchKernelGGL((softmax_whole_reg_kernel<2>), dim3(1), dim3(1024), 0, l.stream, x, y, n);
+    else if (n <= 8192)
+        hipLaunchKernelGGL((softmax_whole_reg_kernel<8>), dim3(1), dim3(1024), 0, l.stream, x, y, n);
+    else
+        hipLaunchKernelGGL(softmax_whole_kernel, dim3(1), dim3(1024), 0, l.stream, x, y, n);
     SHP_HIP_CHECK(hipGetLastError());
     return SHP_OK;
 }

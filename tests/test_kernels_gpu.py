@@ -222,6 +222,10 @@ def test_softmax_kernels(ctx, orc):
     x = rnd(8, 1000, scale=4.0)  # EffNet-Lite0 head: whole-tensor semantics at batch 8
     y, r = both(ctx, orc, "softmax1000", x, None, 8000, [8000])
     assert_close(y, r, 1e-7, 1e-4, "softmax1000")
+    for n in (1000, 1500, 9000):  # one, two and (past 8192) the three-pass kernel's elements
+        x = rnd(n, scale=4.0)
+        y, r = both(ctx, orc, "softmax1000", x, None, n, [n])
+        assert_close(y, r, 1e-7, 1e-4, f"softmax1000 n={n}")
     for rows, cols in [(96 * 128, 128), (3, 32000), (7, 1)]:
         x = rnd(rows, cols, scale=3.0)
         mask = rnd(cols)
@@ -702,7 +706,7 @@ def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, re
 
 
 @pytest.mark.parametrize("b,k,n", [(1, 1280, 1000), (8, 1280, 1000), (32, 2048, 1000),
-                                   (3, 37, 5)])
+                                   (3, 37, 5), (5, 64, 13), (2, 4096, 9)])
 def test_fully_connected(ctx, orc, b, k, n):
     w = np.concatenate([rnd(n * k, scale=0.05), rnd(n)])
     x = rnd(b, k)
