@@ -714,7 +714,8 @@ static const char* kNames[] = {
     "hlo_dot_rank2", "conv2d_nhwc", "dot_general_strided", "depthwise_conv2d",
     "resize_bilinear", "depthwise_conv2d_nhwc", "gemv_nt", "argmax_rows", "gather_rows", "hlo_broadcast",
     "hlo_transpose", "hlo_slice", "hlo_concatenate_into", "hlo_compare", "hlo_select",
-    "hlo_reduce", "hlo_strided_copy", "attention_fused", "nan_count", "inverted_residual_nhwc"};
+    "hlo_reduce", "hlo_strided_copy", "attention_fused", "nan_count", "inverted_residual_nhwc",
+    "conv1x1_gap_nhwc"};
 
 int orc_kernel_count(void) { return (int)(sizeof kNames / sizeof kNames[0]); }
 const char* orc_kernel_name(int i) {
@@ -937,6 +938,30 @@ int orc_run_kernel(const char* name, const float* in0, size_t n0, const float* i
         epilogue(out, n_out, 0, NULL, residual, act, alpha);
         free(ebuf);
         free(dbuf);
+        return 0;
+    }
+    if (!strcmp(name, "conv1x1_gap_nhwc")) {
+        /* The classifier head as the TFLite scheduler dispatches it: CONV_2D 1x1 with its fused
+         * activation (scheduler.rs:321-427), then MEAN over H and W (:549-613) -- the loops of
+         * conv2d_nhwc and global_avg_pool_nhwc above.  push {n, cin, h, w, cout, total}. */
+        NEED(6);
+        const int n = push[0], cin = push[1], h = push[2], w = push[3], cout = push[4];
+        TOTAL((int64_t)n * cout);
+        if (residual) return orc_fail(-4, "conv1x1_gap_nhwc: no residual");
+        const size_t nc = (size_t)n * h * w * cout;
+        float* cbuf = (float*)malloc(sizeof(float) * nc);
+        const int32_t qc[15] = {n, cin, h, w, cout, h, w, 1, 1, 1, 1, 1, 0, 0, (int32_t)nc};
+        k_conv2d(in0, in1, cbuf, qc, 1);
+        epilogue(cbuf, nc, 0, NULL, NULL, act, alpha);
+        const int hw = h * w;
+        for (int64_t i = 0; i < (int64_t)n_out; ++i) {
+            const int64_t b = i / cout;
+            const int ch = (int)(i % cout);
+            float acc = 0.0f;
+            for (int j = 0; j < hw; ++j) acc = acc + cbuf[(b * hw + j) * cout + ch];
+            out[i] = acc / (float)hw;
+        }
+        free(cbuf);
         return 0;
     }
     if (!strcmp(name, "depthwise_conv2d") || !strcmp(name, "depthwise_conv2d_nhwc")) {

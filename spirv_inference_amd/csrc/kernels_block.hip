@@ -878,10 +878,103 @@ extern "C" int shp_block_plan(const int32_t* push, size_t n_push, int32_t* out8)
     return SHP_OK;
 }
 
+namespace {
+
+// ---- conv1x1_gap_nhwc: the classifier head's 1x1 convolution, its activation and the global
+// average pool in one launch (the TFLite graph's CONV_2D + MEAN, scheduler.rs:321-427 and
+// :549-613).  push {n, cin, h, w, cout, total = n * cout}; in1 = [cout][cin] weights + bias
+// tail; the epilogue's activation applies per pixel, before the mean.  A workgroup owns one
+// image and 16 output channels: each wavefront takes 16-pixel row blocks and runs the
+// product on v_mfma_f32_16x16x4_f32 (lane group g reads the K quarter [4g, 4g + 4) of every
+// 16-wide K step, 16 contiguous bytes, for x and the weights alike), two accumulators on
+// alternate K steps; the activated pixels are summed per lane, across the lane groups and
+// across the wavefronts in LDS, and divided by h * w as the reference pool does.  The
+// convolution's output never reaches memory.
+__global__ __launch_bounds__(256) void conv1x1_gap_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          float* __restrict__ y, int cin,
+                                                          int hw, int cout, int cblk, int act,
+                                                          float alpha) {
+    __shared__ float part[4][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, li = lane & 15;
+    const int img = blockIdx.x / cblk, c0 = (blockIdx.x - img * cblk) * 16;
+    const int col = c0 + li;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x + (int64_t)img * hw * cin, (int64_t)hw * cin);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (int64_t)cout * cin + cout);
+    const bool col_ok = col < cout;
+    const unsigned wrow = (unsigned)(col * cin) * 4u;
+    const float bias = col_ok ? w[(int64_t)cout * cin + col] : 0.f;
+    const int nrb = (hw + 15) >> 4;
+    float sum = 0.f;
+    for (int rb = wave; rb < nrb; rb += 4) {
+        const int px = rb * 16 + li;
+        const bool px_ok = px < hw;
+        const unsigned xrow = (unsigned)(px * cin) * 4u;
+        floatx4 e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
+        for (int k0 = 0; k0 < cin; k0 += 32) {
+            const int ka = k0 + 4 * g, kb = ka + 16;
+            const f4v a0 = ld16(xr, px_ok && ka < cin ? xrow + 4u * ka : kOob);
+            const f4v b0 = ld16(wr, col_ok && ka < cin ? wrow + 4u * ka : kOob);
+            const f4v a1 = ld16(xr, px_ok && kb < cin ? xrow + 4u * kb : kOob);
+            const f4v b1 = ld16(wr, col_ok && kb < cin ? wrow + 4u * kb : kOob);
+            e0 = mfma4(a0, b0, e0);
+            e1 = mfma4(a1, b1, e1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // accumulator r: pixel rb * 16 + 4g + r, channel li
+            const float v = shpd::apply_act(e0[r] + e1[r] + bias, act, alpha);
+            sum += rb * 16 + 4 * g + r < hw ? v : 0.f;
+        }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    if (g == 0) part[wave][li] = sum;
+    __syncthreads();
+    if (tid < 16 && c0 + tid < cout)
+        y[(int64_t)img * cout + c0 + tid] =
+            (part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid]) / (float)hw;
+}
+
+int launch_conv1x1_gap(const shp::Launch& l) {
+    if (l.n_push < 6) return shp::fail(SHP_ERR_PUSH, "conv1x1_gap_nhwc needs 6 push constants");
+    const int32_t* q = l.push;
+    const int n = q[0], cin = q[1], h = q[2], wd = q[3], cout = q[4];
+    if (n <= 0 || cin <= 0 || h <= 0 || wd <= 0 || cout <= 0)
+        return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: non-positive dim");
+    if ((int64_t)q[5] != (int64_t)n * cout)
+        return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: total != n*cout");
+    int rc = shp::check_total(l, (int64_t)n * cout, "conv1x1_gap_nhwc");
+    if (rc) return rc;
+    if (l.epi->bias || l.epi->residual)
+        return shp::fail(SHP_ERR_INVALID,
+                         "conv1x1_gap_nhwc: the bias is the weights' tail; no residual");
+    auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (cin % 4 || !l.in0 || !l.in1 || !a16(l.in0) || !a16(l.in1))
+        return shp::fail(SHP_ERR_UNSUPPORTED,
+                         "conv1x1_gap_nhwc: cin must be a multiple of 4, x and weights 16-byte "
+                         "aligned");
+    // buffer loads with 32-bit byte offsets over one image of x and over the weights
+    const int64_t hw = (int64_t)h * wd;
+    if (hw * cin * 4 >= (1ll << 31) || ((int64_t)cout * cin + cout) * 4 >= (1ll << 31))
+        return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: tensors too large");
+    const int cblk = (cout + 15) / 16;
+    if ((int64_t)n * cblk >= (1ll << 31))
+        return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: grid too large");
+    hipLaunchKernelGGL(conv1x1_gap_kernel, dim3((unsigned)(n * cblk)), dim3(256), 0, l.stream,
+                       (const float*)l.in0, (const float*)l.in1, (float*)l.out, cin, (int)hw,
+                       cout, cblk, l.epi->act, l.epi->alpha);
+    SHP_HIP_CHECK(hipGetLastError());
+    return SHP_OK;
+}
+
+}  // namespace
+
 namespace shp {
 
 KernelEntry kBlockKernels[] = {
     {"inverted_residual_nhwc", 16, true, launch_ir},
+    {"conv1x1_gap_nhwc", 6, true, launch_conv1x1_gap},
 };
 const int kBlockKernelCount = sizeof(kBlockKernels) / sizeof(kBlockKernels[0]);
 

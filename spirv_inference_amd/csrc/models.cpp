@@ -335,6 +335,21 @@ Act4 tfl_block(Model& m, Act4 x, int expand, int k, int s, int cout, bool residu
     return Act4{y, x.n, oh, ow, cout};
 }
 
+// The classifier head's 1x1 conv + ReLU6 + global average pool as one launch; returns the
+// pooled [n][oc] tensor.
+int tfl_head(Model& m, Act4 x, int oc, const char* label) {
+    const uint64_t K = (uint64_t)x.c;
+    int w = m.tensor(K * oc + oc, 1);
+    m.fill_normal(w, 0, K * oc, std::sqrt(2.0f / (float)K));
+    m.fill_normal(w, K * oc, oc, 0.01f);
+    m.weight_bytes += (double)(K * oc + oc) * 4.0;
+    int y = m.tensor((uint64_t)x.n * oc);
+    m.op("conv1x1_gap_nhwc", x.t, w, y, {x.n, x.c, x.h, x.w, oc, x.n * oc}, -1, -1,
+         SHP_ACT_RELU6, 0.0f, label);
+    m.flops += 2.0 * (double)x.n * x.h * x.w * oc * K;
+    return y;
+}
+
 int tfl_net(Model& m, int batch, const MBConv* cfg, int ncfg, int stem_c) {
     const int n = batch;
     int in = m.tensor((uint64_t)n * 224 * 224 * 3, 2);
@@ -371,9 +386,18 @@ int tfl_net(Model& m, int batch, const MBConv* cfg, int ncfg, int stem_c) {
             x = tfl_conv(m, h, cfg[i].c, 1, 1, SHP_ACT_NONE, res ? in_x.t : -1, label);
         }
     }
-    x = tfl_conv(m, x, 1280, 1, 1, SHP_ACT_RELU6, -1, "head_conv");
-    int gap = m.tensor((uint64_t)n * 1280);
-    m.op("global_avg_pool_nhwc", x.t, -1, gap, {n, x.h, x.w, 1280}, -1, -1, 0, 0.0f, "avg_pool");
+    int gap;
+    if (m.ctx->tune.ir_fuse >= 0) {
+        // the head's 1x1 conv + ReLU6 and the global average pool as one conv1x1_gap_nhwc
+        // launch (weights filled as tfl_conv fills them, so they equal the two-operator
+        // graph's of the same seed); the three-operator build keeps the reference's two
+        gap = tfl_head(m, x, 1280, "head_conv_pool");
+    } else {
+        x = tfl_conv(m, x, 1280, 1, 1, SHP_ACT_RELU6, -1, "head_conv");
+        gap = m.tensor((uint64_t)n * 1280);
+        m.op("global_avg_pool_nhwc", x.t, -1, gap, {n, x.h, x.w, 1280}, -1, -1, 0, 0.0f,
+             "avg_pool");
+    }
     int fw = m.tensor(1280 * 1000 + 1000, 1);
     m.fill_normal(fw, 0, 1280 * 1000, std::sqrt(2.0f / 1280.0f));
     m.fill_normal(fw, 1280 * 1000, 1000, 0.01f);

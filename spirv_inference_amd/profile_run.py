@@ -49,6 +49,8 @@ def op_work(op, elems) -> tuple[float, float]:
         px_in, px_out = q[0] * q[2] * q[3], q[0] * q[6] * q[7]
         flops = 2.0 * (px_in * q[1] * q[4] * q[12] + px_out * q[4] * q[8] * q[8] +
                        px_out * q[4] * q[5])
+    elif k == "conv1x1_gap_nhwc":  # {n, cin, h, w, cout, total}
+        flops = 2.0 * q[0] * q[2] * q[3] * q[1] * q[4]
     nbytes = 4.0 * (sum(ins) + op.out_elems + extra)
     return flops, nbytes
 

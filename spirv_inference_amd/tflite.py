@@ -601,7 +601,9 @@ class TfliteExecutor:
     1x1 CONV_2D [-> residual ADD], whose intermediates nothing else reads, runs as one
     inverted_residual_nhwc launch at the projection where the library expects that to beat
     the three launches (shp_block_plan); fuse_blocks=True fuses every chain the kernel takes,
-    False none.  Anything else raises, like the reference's scheduler.
+    False none.  A 1x1 CONV_2D read only by a global pool (the classifier head) runs as one
+    conv1x1_gap_nhwc launch unless fuse_blocks is False.  Anything else raises, like the
+    reference's scheduler.
 
     run(graph=True) replays the launch sequence from one hipGraph: the first such call runs
     eagerly if nothing ran yet (so every buffer, packed weight and split-K workspace exists),
@@ -628,6 +630,7 @@ class TfliteExecutor:
         self._check_aliases()
         self.residual_adds = self._find_residual_adds()
         self.blocks = self._find_blocks(fuse_blocks is None) if fuse_blocks is not False else {}
+        self.heads = self._find_heads() if fuse_blocks is not False else {}
         self._graph = None
         self._warm = False
 
@@ -740,6 +743,61 @@ class TfliteExecutor:
                 continue
             out[pi] = blk
         return out
+
+    def _find_heads(self) -> Dict[int, int]:
+        """{pool operator index: conv operator index} for every classifier head the fused
+        conv1x1_gap_nhwc kernel takes: a 1x1 stride-1 CONV_2D with constant weights and bias,
+        no dilation, ReLU / ReLU6 / no activation and a channel count that is a multiple of
+        4, whose output only a global pool reads (MEAN over H and W, or an AVERAGE_POOL_2D
+        over the whole map without an activation of its own) and is not a model output."""
+        readers = {}
+        for op in self.model.operators:
+            for t in op.inputs:
+                readers.setdefault(t, []).append(op.index)
+        ops = self.model.operators
+        out = {}
+        for conv in ops:
+            if conv.builtin != "CONV_2D" or conv.inputs[1] not in self.consts:
+                continue
+            if len(conv.inputs) > 2 and conv.inputs[2] >= 0 and conv.inputs[2] not in self.consts:
+                continue
+            o = decode_options(conv)
+            _, kh, kw, cin = self._shape(conv.inputs[1])
+            if ((kh, kw, o["stride_h"], o["stride_w"], o["dilation_h_factor"],
+                 o["dilation_w_factor"]) != (1, 1, 1, 1, 1, 1)
+                    or o["fused_activation"] not in ("none", "relu", "relu6") or cin % 4):
+                continue
+            t = conv.outputs[0]
+            r = readers.get(t, [])
+            if len(r) != 1 or t in self.model.outputs:
+                continue
+            pool = ops[r[0]]
+            if pool.inputs[0] != t or len(self._shape(t)) != 4:
+                continue
+            n, h, w_, c = self._shape(t)
+            if self._elems(pool.outputs[0]) != n * c:
+                continue
+            if pool.builtin == "MEAN":
+                if sorted(int(a) % 4 for a in self.consts.get(pool.inputs[1], [])) != [1, 2]:
+                    continue
+            elif pool.builtin == "AVERAGE_POOL_2D":
+                po = decode_options(pool)
+                if (po["filter_h"], po["filter_w"], po["fused_activation"]) != (h, w_, "none"):
+                    continue
+            else:
+                continue
+            out[pool.index] = conv.index
+        return out
+
+    def _run_head(self, pool: Operator, ci: int) -> None:
+        conv = self.model.operators[ci]
+        n, h, w_, cin = self._shape(conv.inputs[0])
+        cout = self._shape(conv.inputs[1])[0]
+        w = self._pack(conv.inputs[1], conv.inputs[2] if len(conv.inputs) > 2 else -1, cout)
+        y = self._alloc(pool.outputs[0])
+        self._launch("conv1x1_gap_nhwc", self._get(conv.inputs[0]), w, y,
+                     [n, cin, h, w_, cout, n * cout],
+                     act=decode_options(conv)["fused_activation"])
 
     def _block_push(self, proj: Operator, blk: dict) -> List[int]:
         from ._lib import ACT
@@ -888,6 +946,8 @@ class TfliteExecutor:
             fused[blk["dw"]] = pi
             if blk["expand"] is not None:
                 fused[blk["expand"]] = pi
+        for pool, conv in self.heads.items():
+            fused[conv] = pool
         for oi in self.order:
             op = self.model.operators[oi]
             self.op_log.append({"index": op.index, "op": op.builtin,
@@ -898,6 +958,9 @@ class TfliteExecutor:
                 continue
             if op.index in self.blocks:
                 self._run_block(op, self.blocks[op.index])
+                continue
+            if op.index in self.heads:
+                self._run_head(op, self.heads[op.index])
                 continue
             self._run_op(op, self.op_log[-1]["options"])
 
@@ -1096,10 +1159,11 @@ _ACT_TO_TFL = {0: 0, 1: 1, 2: 3, 5: 4}  # registry epilogue code -> ActivationFu
 def model_to_tflite(m, description: str = "") -> bytes:
     """A TFL3 file of a resident model graph built on the TFLite path (MobileNetV2,
     EfficientNet-Lite0: conv2d_nhwc, depthwise_conv2d_nhwc or the fused
-    inverted_residual_nhwc, global_avg_pool_nhwc, fully_connected, softmax1000), with its
-    weights: CONV_2D / DEPTHWISE_CONV_2D (OHWI and [1,KH,KW,C] weights with separate bias
-    tensors; a fused block as its three operators), ADD for a residual the graph fuses into
-    a convolution, MEAN over H and W, FULLY_CONNECTED, SOFTMAX."""
+    inverted_residual_nhwc, global_avg_pool_nhwc or the fused conv1x1_gap_nhwc head,
+    fully_connected, softmax1000), with its weights: CONV_2D / DEPTHWISE_CONV_2D (OHWI and
+    [1,KH,KW,C] weights with separate bias tensors; a fused block as its three operators, a
+    fused head as CONV_2D + MEAN), ADD for a residual the graph fuses into a convolution, MEAN
+    over H and W, FULLY_CONNECTED, SOFTMAX."""
     w = TfliteWriter(description or f"{m.arch} exported from the resident graph")
     tfl: Dict[int, int] = {}          # model tensor id -> tflite tensor index
     host = lambda tid: m.download(tid)
@@ -1166,6 +1230,17 @@ def model_to_tflite(m, description: str = "") -> bytes:
             tfl[op.out] = conv(f"{base}_project", x, n, ce, oh, ow, cout, 1, 1, True,
                                packed[o:o + cout * ce], packed[o + cout * ce:o + cout * ce + cout],
                                _ACT_TO_TFL[op.act], tfl[op.residual] if op.residual >= 0 else None)
+        elif op.kernel == "conv1x1_gap_nhwc":  # the fused head: CONV_2D 1x1, then MEAN
+            n, cin, h, w_, cout = q[:5]
+            packed = host(op.in1)
+            x = model_input(op.in0, [n, h, w_, cin])
+            base = op.label[:-len("_pool")] if op.label.endswith("_pool") else op.label
+            y = conv(base, x, n, cin, h, w_, cout, 1, 1, True, packed[:cout * cin],
+                     packed[cout * cin:cout * cin + cout], _ACT_TO_TFL[op.act])
+            axes = w.tensor(f"{op.label}/axes", [2], np.array([1, 2], np.int32).view(np.float32),
+                            ttype=2)
+            tfl[op.out] = w.tensor(op.label, [n, cout])
+            w.op("MEAN", [y, axes], [tfl[op.out]], "ReducerOptions", {0: ("B", 0)})
         elif op.kernel == "global_avg_pool_nhwc":
             n, h, w_, c = q[:4]
             axes = w.tensor(f"{op.label}/axes", [2], np.array([1, 2], np.int32).view(np.float32),

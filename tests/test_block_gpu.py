@@ -151,3 +151,47 @@ def test_rejects_what_it_does_not_handle(ctx):
     bad[15] += 1
     with pytest.raises(ShpError, match="total"):
         run_block(ctx, x, packed, bad)
+
+
+HEADS = [  # (label, n, cin, h, w, cout, act)
+    ("mbv2_head_b1", 1, 320, 7, 7, 1280, RELU6),
+    ("effnet_head_b8", 8, 320, 7, 7, 1280, RELU6),
+    ("odd", 3, 20, 5, 3, 40, 1),
+    ("one_pixel", 2, 8, 1, 1, 16, 0),
+    ("two_rounds", 1, 36, 12, 11, 24, RELU6),  # 132 pixels: wavefronts take two row blocks
+]
+
+
+@pytest.mark.parametrize("case", HEADS, ids=[c[0] for c in HEADS])
+def test_conv1x1_gap_matches_conv_then_pool(ctx, orc, case):
+    """conv1x1_gap_nhwc (1x1 conv + activation + global average pool in one launch) against
+    the oracle's conv2d_nhwc + global_avg_pool_nhwc chain at the build's 1e-4 gate."""
+    label, n, cin, h, w, cout, act = case
+    print(f"[head] {label}", flush=True)
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-1, 1, n * h * w * cin).astype(np.float32)
+    wt = np.concatenate([rng.standard_normal(cout * cin) * np.sqrt(2.0 / cin),
+                         rng.standard_normal(cout) * 0.1]).astype(np.float32)
+    push = [n, cin, h, w, cout, n * cout]
+    dx, dw, dy = ctx.tensor(x), ctx.tensor(wt), ctx.empty(n * cout)
+    try:
+        ctx.launch("conv1x1_gap_nhwc", dx, dw, dy, push, act=act)
+        ctx.sync()
+        got = dy.download()
+    finally:
+        for t in (dx, dw, dy):
+            t.free()
+    ref = orc.run("conv1x1_gap_nhwc", x, wt, n * cout, push, act=act)
+    from conftest import assert_close
+    assert_close(got, ref, what=label)
+
+
+def test_conv1x1_gap_rejects(ctx):
+    x = np.zeros(2 * 7 * 7 * 6, np.float32)
+    with pytest.raises(ShpError, match="multiple of 4"):
+        ctx_run = ctx.tensor(x), ctx.tensor(np.zeros(16 * 6 + 16, np.float32)), ctx.empty(32)
+        try:
+            ctx.launch("conv1x1_gap_nhwc", *ctx_run, [2, 6, 7, 7, 16, 32])
+        finally:
+            for t in ctx_run:
+                t.free()

@@ -467,3 +467,22 @@ def test_inverted_residual_vs_float64(orc, expand, k, s, res):
     if res:
         Y = Y + X
     assert_close(got, Y.reshape(-1), 2e-6, 2e-6, "inverted_residual_nhwc")
+
+
+@pytest.mark.parametrize("act,h,w", [("relu6", 7, 7), ("none", 3, 5), ("relu", 1, 1)])
+def test_conv1x1_gap_vs_float64(orc, act, h, w):
+    """conv1x1_gap_nhwc (the head's 1x1 convolution, its activation and the global average
+    pool in one call) against a float64 einsum, clip and mean; relu6 with values spread past
+    6 so the clamp matters, and a 1x1 map where the mean is the pixel itself."""
+    rng = np.random.default_rng(5)
+    n, cin, cout = 2, 12, 20
+    x = (rng.standard_normal(n * h * w * cin) * 2).astype(np.float32)
+    wt = (rng.standard_normal((cout, cin)) * 0.8).astype(np.float32)
+    b = (rng.standard_normal(cout) * 0.5).astype(np.float32)
+    got = orc.run("conv1x1_gap_nhwc", x, np.concatenate([wt.reshape(-1), b]), n * cout,
+                  [n, cin, h, w, cout, n * cout], act=act)
+    C = np.einsum("npc,oc->npo", x.reshape(n, h * w, cin).astype(np.float64), wt) + b
+    if act == "relu6":
+        assert (C > 6).any() and (C < 0).any()
+    C = {"relu6": np.clip(C, 0, 6), "relu": np.maximum(C, 0), "none": C}[act]
+    assert_close(got, C.mean(axis=1).reshape(-1), 2e-6, 2e-6, "conv1x1_gap_nhwc")

@@ -336,3 +336,53 @@ def test_executor_keeps_chains_it_cannot_fuse(extra):
 def test_executor_needs_channel_multiples_for_a_block():
     m, _ = _mbconv_model(cin=6, ce=24, cout=6)  # cin % 4 != 0, ce % 16 != 0
     assert T.TfliteExecutor(_NoDevice(), m, fuse_blocks=True).blocks == {}
+
+
+def _head_model(cin=8, cout=12, k=1, pool="MEAN", axes=(1, 2), conv_out=False, act=3,
+                pool_act=0):
+    """x -> CONV_2D k x k (act) -> global pool (MEAN over axes, or AVERAGE_POOL_2D over the
+    whole map with pool_act) -> FULLY_CONNECTED; conv_out also makes the convolution's output
+    a model output."""
+    rng = np.random.default_rng(1)
+    w = T.TfliteWriter()
+    h = 5
+    x = w.tensor("x", [1, h, h, cin])
+    w.inputs = [x]
+    wc = w.tensor("wc", [cout, k, k, cin], rng.standard_normal(cout * k * k * cin).astype(np.float32))
+    bc = w.tensor("bc", [cout], rng.standard_normal(cout).astype(np.float32))
+    c = w.tensor("c", [1, h, h, cout])
+    ops = {"conv": w.op("CONV_2D", [x, wc, bc], [c], "Conv2DOptions",
+                        {0: ("b", 0), 1: ("i", 1), 2: ("i", 1), 3: ("b", act)})}
+    p = w.tensor("p", [1, cout])
+    if pool == "MEAN":
+        ax = w.tensor("axes", [len(axes)], np.array(axes, np.int32).view(np.float32), ttype=2)
+        ops["pool"] = w.op("MEAN", [c, ax], [p], "ReducerOptions", {0: ("B", 0)})
+    else:
+        ops["pool"] = w.op("AVERAGE_POOL_2D", [c], [p], "Pool2DOptions",
+                           {0: ("b", 1), 1: ("i", 1), 2: ("i", 1), 3: ("i", h), 4: ("i", h),
+                            5: ("b", pool_act)})
+    wf = w.tensor("wf", [3, cout], rng.standard_normal(3 * cout).astype(np.float32))
+    f = w.tensor("f", [1, 3])
+    w.op("FULLY_CONNECTED", [p, wf, -1], [f], "FullyConnectedOptions", {0: ("b", 0)})
+    w.outputs = [f] + ([c] if conv_out else [])
+    return T.parse_model(w.finish()), ops
+
+
+@pytest.mark.parametrize("kw,fuses", [({}, True), ({"pool": "AVERAGE_POOL_2D"}, True),
+                                      ({"act": 0}, True), ({"k": 3}, False),
+                                      ({"conv_out": True}, False), ({"axes": (1,)}, False),
+                                      ({"cin": 6}, False),
+                                      ({"pool": "AVERAGE_POOL_2D", "pool_act": 1}, False)])
+def test_executor_fuses_the_classifier_head(kw, fuses):
+    """A 1x1 CONV_2D read only by a global pool runs as one conv1x1_gap_nhwc launch (by
+    default, and not with fuse_blocks=False); 3x3 kernels, a convolution output that is a
+    model output, a MEAN over H only, a channel count off the multiple of 4 and a pool with
+    an activation of its own keep the two operators."""
+    try:
+        m, ops = _head_model(**kw)
+    except ValueError:
+        assert not fuses  # a MEAN over one axis may not even describe a [1, C] output
+        return
+    want = {ops["pool"]: ops["conv"]} if fuses else {}
+    assert T.TfliteExecutor(_NoDevice(), m).heads == want
+    assert T.TfliteExecutor(_NoDevice(), m, fuse_blocks=False).heads == {}
