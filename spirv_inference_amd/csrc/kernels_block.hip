@@ -887,9 +887,10 @@ namespace {
 // image and 16 output channels: each wavefront takes 16-pixel row blocks and runs the
 // product on v_mfma_f32_16x16x4_f32 (lane group g reads the K quarter [4g, 4g + 4) of every
 // 16-wide K step, 16 contiguous bytes, for x and the weights alike), two accumulators on
-// alternate K steps; the activated pixels are summed per lane, across the lane groups and
-// across the wavefronts in LDS, and divided by h * w as the reference pool does.  The
-// convolution's output never reaches memory.
+// alternate K steps, operands loaded eight K steps at a time one group ahead; the activated
+// pixels are summed per lane, across the lane groups and across the wavefronts in LDS, and
+// divided by h * w as the reference pool does.  The convolution's output never reaches
+// memory.
 __global__ __launch_bounds__(256) void conv1x1_gap_kernel(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           float* __restrict__ y, int cin,
@@ -907,19 +908,37 @@ __global__ __launch_bounds__(256) void conv1x1_gap_kernel(const float* __restric
     const float bias = col_ok ? w[(int64_t)cout * cin + col] : 0.f;
     const int nrb = (hw + 15) >> 4;
     float sum = 0.f;
+    constexpr int G = 8;  // 16-wide K steps per load group (K 128)
     for (int rb = wave; rb < nrb; rb += 4) {
         const int px = rb * 16 + li;
         const bool px_ok = px < hw;
         const unsigned xrow = (unsigned)(px * cin) * 4u;
         floatx4 e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
-        for (int k0 = 0; k0 < cin; k0 += 32) {
-            const int ka = k0 + 4 * g, kb = ka + 16;
-            const f4v a0 = ld16(xr, px_ok && ka < cin ? xrow + 4u * ka : kOob);
-            const f4v b0 = ld16(wr, col_ok && ka < cin ? wrow + 4u * ka : kOob);
-            const f4v a1 = ld16(xr, px_ok && kb < cin ? xrow + 4u * kb : kOob);
-            const f4v b1 = ld16(wr, col_ok && kb < cin ? wrow + 4u * kb : kOob);
-            e0 = mfma4(a0, b0, e0);
-            e1 = mfma4(a1, b1, e1);
+        // a group's 2 x G loads go out together, and the next group's before this group's
+        // products, so the L2 round trips overlap instead of one per K step
+        f4v xa[G], wb[G];
+        auto load = [&](f4v (&xv)[G], f4v (&wv)[G], int k0) {
+#pragma unroll
+            for (int c = 0; c < G; ++c) {
+                const int k = k0 + 16 * c + 4 * g;
+                xv[c] = ld16(xr, px_ok && k < cin ? xrow + 4u * k : kOob);
+                wv[c] = ld16(wr, col_ok && k < cin ? wrow + 4u * k : kOob);
+            }
+        };
+        load(xa, wb, 0);
+        for (int k0 = 0; k0 < cin; k0 += 16 * G) {
+            f4v xn[G], wn[G];
+            if (k0 + 16 * G < cin) load(xn, wn, k0 + 16 * G);
+#pragma unroll
+            for (int c = 0; c < G; c += 2) {
+                e0 = mfma4(xa[c], wb[c], e0);
+                e1 = mfma4(xa[c + 1], wb[c + 1], e1);
+            }
+#pragma unroll
+            for (int c = 0; c < G; ++c) {
+                xa[c] = xn[c];
+                wb[c] = wn[c];
+            }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {  // accumulator r: pixel rb * 16 + 4g + r, channel li
@@ -932,6 +951,86 @@ __global__ __launch_bounds__(256) void conv1x1_gap_kernel(const float* __restric
     if (g == 0) part[wave][li] = sum;
     __syncthreads();
     if (tid < 16 && c0 + tid < cout)
+        y[(int64_t)img * cout + c0 + tid] =
+            (part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid]) / (float)hw;
+}
+
+// The same head for maps of at most 64 pixels and at most 512 input channels (the 7x7
+// heads), with the K steps split over the wavefronts instead of the row blocks: wavefront w
+// takes the 16-wide K steps w, w + 4, ... for all four row blocks and CB column blocks, and
+// issues every operand load of its share at once (one round trip to L2 / HBM instead of one
+// per load group); the four partial products meet in LDS, summed in wavefront order, and
+// wavefront r then finishes row block r as the kernel above does.
+template <int CB>
+__global__ __launch_bounds__(256) void conv1x1_gap_small_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                float* __restrict__ y, int cin,
+                                                                int hw, int cout, int cblk,
+                                                                int act, float alpha) {
+    constexpr int NK = 8;  // K steps per wavefront: cin <= 4 * 16 * NK
+    __shared__ f4v red[4][4][CB][64];
+    __shared__ float part[4][16 * CB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, li = lane & 15;
+    const int img = blockIdx.x / cblk, c0 = (blockIdx.x - img * cblk) * 16 * CB;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x + (int64_t)img * hw * cin, (int64_t)hw * cin);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (int64_t)cout * cin + cout);
+    const int nch = (cin + 15) >> 4;
+    f4v xa[NK][4], wb[NK][CB];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        const int k = 16 * (wave + 4 * i) + 4 * g;
+        const bool kok = k < cin;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int px = rb * 16 + li;
+            xa[i][rb] = ld16(xr, kok && px < hw ? (unsigned)(px * cin + k) * 4u : kOob);
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const int col = c0 + cb * 16 + li;
+            wb[i][cb] = ld16(wr, kok && col < cout ? (unsigned)(col * cin + k) * 4u : kOob);
+        }
+    }
+    floatx4 acc[4][CB];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        if (wave + 4 * i < nch) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = mfma4(xa[i][rb], wb[i][cb], acc[rb][cb]);
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            red[wave][rb][cb][lane] = f4v{acc[rb][cb][0], acc[rb][cb][1], acc[rb][cb][2], acc[rb][cb][3]};
+    __syncthreads();
+    const int rb = wave;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int col = c0 + cb * 16 + li;
+        const float bias = col < cout ? w[(int64_t)cout * cin + col] : 0.f;
+        const f4v v = red[0][rb][cb][lane] + red[1][rb][cb][lane] + red[2][rb][cb][lane] +
+                      red[3][rb][cb][lane];
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // pixel rb * 16 + 4g + r, channel li of block cb
+            const float a = shpd::apply_act(v[r] + bias, act, alpha);
+            sum += rb * 16 + 4 * g + r < hw ? a : 0.f;
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        if (g == 0) part[rb][cb * 16 + li] = sum;
+    }
+    __syncthreads();
+    if (tid < 16 * CB && c0 + tid < cout)
         y[(int64_t)img * cout + c0 + tid] =
             (part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid]) / (float)hw;
 }
@@ -961,6 +1060,21 @@ int launch_conv1x1_gap(const shp::Launch& l) {
     const int cblk = (cout + 15) / 16;
     if ((int64_t)n * cblk >= (1ll << 31))
         return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: grid too large");
+    if (hw <= 64 && cin <= 512) {
+        // two column blocks per workgroup once that still leaves >= 512 workgroups
+        const int cb2 = (cout + 31) / 32;
+        if ((int64_t)n * cb2 >= 512) {
+            hipLaunchKernelGGL((conv1x1_gap_small_kernel<2>), dim3((unsigned)(n * cb2)), dim3(256),
+                               0, l.stream, (const float*)l.in0, (const float*)l.in1,
+                               (float*)l.out, cin, (int)hw, cout, cb2, l.epi->act, l.epi->alpha);
+        } else {
+            hipLaunchKernelGGL((conv1x1_gap_small_kernel<1>), dim3((unsigned)(n * cblk)), dim3(256),
+                               0, l.stream, (const float*)l.in0, (const float*)l.in1,
+                               (float*)l.out, cin, (int)hw, cout, cblk, l.epi->act, l.epi->alpha);
+        }
+        SHP_HIP_CHECK(hipGetLastError());
+        return SHP_OK;
+    }
     hipLaunchKernelGGL(conv1x1_gap_kernel, dim3((unsigned)(n * cblk)), dim3(256), 0, l.stream,
                        (const float*)l.in0, (const float*)l.in1, (float*)l.out, cin, (int)hw,
                        cout, cblk, l.epi->act, l.epi->alpha);

@@ -1464,13 +1464,22 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
     const bool vec = (K % 4 == 0) && (((uintptr_t)w & 15) == 0) && (((uintptr_t)x & 15) == 0);
     if (vec) {
-        for (int k = lane * 4; k < K; k += 256) {
-            float4 wv = *reinterpret_cast<const float4*>(wr + k);
+        // four 256-wide K steps' weight loads go out together (one HBM round trip per four
+        // steps, not per step); the sums still run in K order
+        for (int k0 = lane * 4; k0 < K; k0 += 1024) {
+            float4 wv[4];
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                if (m < M) {
-                    float4 xv = *reinterpret_cast<const float4*>(x + (int64_t)m * K + k);
-                    acc[m] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+            for (int j = 0; j < 4; ++j)
+                if (k0 + 256 * j < K) wv[j] = *reinterpret_cast<const float4*>(wr + k0 + 256 * j);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + 256 * j;
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    if (m < M && k < K) {
+                        float4 xv = *reinterpret_cast<const float4*>(x + (int64_t)m * K + k);
+                        acc[m] += wv[j].x * xv.x + wv[j].y * xv.y + wv[j].z * xv.z + wv[j].w * xv.w;
+                    }
                 }
             }
         }
@@ -1506,8 +1515,15 @@ __global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restr
                                                             int K, const float* __restrict__ bias,
                                                             int act, float alpha) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [M][K]
-    for (int i = threadIdx.x * 4; i < M * K; i += 1024)
-        *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+    for (int i0 = threadIdx.x * 4; i0 < M * K; i0 += 8192) {  // 8 loads in flight per thread
+        f4v t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (i0 + 1024 * u < M * K) t[u] = *reinterpret_cast<const f4v*>(x + i0 + 1024 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (i0 + 1024 * u < M * K) *reinterpret_cast<f4v*>(xs + i0 + 1024 * u) = t[u];
+    }
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int n0 = blockIdx.x * 8 + 2 * (threadIdx.x >> 6);
@@ -1518,15 +1534,25 @@ __global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restr
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) a0[m] = a1[m] = 0.0f;
-    for (int k = lane * 4; k < K; k += 256) {
-        const float4 u = *reinterpret_cast<const float4*>(w0 + k);
-        const float4 v = *reinterpret_cast<const float4*>(w1 + k);
+    for (int k0 = lane * 4; k0 < K; k0 += 1024) {  // four K steps' weights in flight
+        f4v u[4], v[4];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            if (m < M) {
-                const float4 xv = *reinterpret_cast<const float4*>(xs + m * K + k);
-                a0[m] += u.x * xv.x + u.y * xv.y + u.z * xv.z + u.w * xv.w;
-                a1[m] += v.x * xv.x + v.y * xv.y + v.z * xv.z + v.w * xv.w;
+        for (int j = 0; j < 4; ++j) {
+            if (k0 + 256 * j < K) {
+                u[j] = *reinterpret_cast<const f4v*>(w0 + k0 + 256 * j);
+                v[j] = *reinterpret_cast<const f4v*>(w1 + k0 + 256 * j);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = k0 + 256 * j;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m < M && k < K) {
+                    const f4v xv = *reinterpret_cast<const f4v*>(xs + m * K + k);
+                    a0[m] += u[j].x * xv.x + u[j].y * xv.y + u[j].z * xv.z + u[j].w * xv.w;
+                    a1[m] += v[j].x * xv.x + v[j].y * xv.y + v[j].z * xv.z + v[j].w * xv.w;
+                }
             }
         }
     }

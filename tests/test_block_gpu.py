@@ -159,13 +159,17 @@ HEADS = [  # (label, n, cin, h, w, cout, act)
     ("odd", 3, 20, 5, 3, 40, 1),
     ("one_pixel", 2, 8, 1, 1, 16, 0),
     ("two_rounds", 1, 36, 12, 11, 24, RELU6),  # 132 pixels: wavefronts take two row blocks
+    ("b16_two_col_blocks", 16, 320, 7, 7, 1280, RELU6),  # 640 workgroups of 32 channels
+    ("k_past_512", 2, 516, 3, 3, 32, RELU6),  # the row-block kernel: cin > 512
 ]
 
 
 @pytest.mark.parametrize("case", HEADS, ids=[c[0] for c in HEADS])
 def test_conv1x1_gap_matches_conv_then_pool(ctx, orc, case):
     """conv1x1_gap_nhwc (1x1 conv + activation + global average pool in one launch) against
-    the oracle's conv2d_nhwc + global_avg_pool_nhwc chain at the build's 1e-4 gate."""
+    the oracle's conv2d_nhwc + global_avg_pool_nhwc chain at the build's 1e-4 gate: maps of
+    at most 64 pixels with K split over the wavefronts (one or two 16-channel column blocks
+    per workgroup), and larger maps or more than 512 input channels on the row-block kernel."""
     label, n, cin, h, w, cout, act = case
     print(f"[head] {label}", flush=True)
     rng = np.random.default_rng(9)
