@@ -321,9 +321,11 @@ int shp_workspace_info(shp_ctx* ctx, void** dptr, uint64_t* bytes) {
     return SHP_OK;
 }
 
-// Force parts of the dense-kernel planner's choice for launches on this context only
-// (0 restores the automatic choice): gemm_tile, gemm_bk, gemm_splits, gemm_dma, gemm_pg,
-// gemm_table, gemm_bl, gemm_sk, gemm_stem, gemm_group, dw_tile.
+// Force parts of the planners' choices for launches on this context only (0 restores the
+// automatic choice): gemm_tile, gemm_bk, gemm_splits, gemm_dma, gemm_pg, gemm_table, gemm_bl,
+// gemm_sk, gemm_stem, gemm_group, dw_tile; the fused block's ir_th, ir_tw, ir_splits,
+// ir_cout_splits and the model graphs' ir_fuse; conv_direct (-1: small-channel 3x3
+// conv2d_nhwc on the implicit GEMM instead of the direct kernel).
 int shp_tune(shp_ctx* ctx, const char* key, int value) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_tune: null ctx");
     shp::GemmTune& t = reinterpret_cast<Ctx*>(ctx)->tune;
