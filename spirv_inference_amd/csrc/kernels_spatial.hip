@@ -572,7 +572,8 @@ int conv_nhwc_direct(const Launch& l) {
     const int64_t dmax = std::max<int64_t>(d.ocg, std::max(d.ow, d.oh));
     // one image's input within the buffer loads' 32-bit byte offsets; the multiply-high
     // divisions exact for every thread index
-    if ((int64_t)d.h * d.w * ci * 4 >= (1ll << 31) || (total + 1) * dmax > (1ll << 32))
+    if ((int64_t)d.h * d.w * ci * 4 >= (1ll << 31) || total >= (1ll << 31) ||
+        (total + 1) * dmax > (1ll << 32))
         return SHP_ERR_UNSUPPORTED;
     d.total = (int)total;
     d.m_ocg = (unsigned)(0xFFFFFFFFull / (uint64_t)d.ocg);
