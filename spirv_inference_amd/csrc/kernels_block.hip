@@ -52,18 +52,20 @@ constexpr int kMaxLds = 160 * 1024;
 
 // LDS layout (float offsets) of one workgroup, shared by the host plan and the kernel:
 // halo patch | We chunk | be | Wd taps | bd | E | D | Wp chunk | halo-row validity | flag.
+// Without an expand there is no halo patch or We: E holds the chunk's 32 input channels of
+// the halo, staged from x chunk by chunk.
 struct IrLds {
     int x, w, be, wd, bd, e, d, wp, hv, flag, total;
 };
 __host__ __device__ inline IrLds ir_lds(int hpb, int xs, int expand, int k, int pb, int ob) {
     IrLds l;
     int o = 0;
-    l.x = o;    o += hpb * 16 * xs;
+    l.x = o;    o += expand ? hpb * 16 * xs : 0;
     l.w = o;    o += expand ? CC * xs : 0;
     l.be = o;   o += CC;
     l.wd = o;   o += k * k * CC;
     l.bd = o;   o += CC;
-    l.e = o;    o += expand ? hpb * 16 * ES : 0;
+    l.e = o;    o += hpb * 16 * ES;  // without expand: the chunk's 32 channels of the halo
     l.d = o;    o += pb * 16 * DS;
     l.wp = o;   o += ob * 16 * WPS;
     l.hv = o;   o += hpb * 16;
@@ -176,8 +178,12 @@ __device__ __forceinline__ floatx4 mfma4(f4v a, f4v b, floatx4 c) {
 }
 
 // K, ST: depthwise kernel size and stride; NBW: projection blocks (16 pixels x 16 output
-// channels) per wavefront, at most.
-template <int K, int ST, int NBW>
+// channels) per wavefront, at most; EXP: the block has an expand (a.expand, as a constant).
+// Without one the input already has the expanded channels: each chunk's 32 of them are staged
+// over the halo from x (UH float4 per thread, loaded during the previous chunk), so the LDS
+// never holds all channels and the depthwise reads them as it reads E.
+constexpr int UH = 5;  // halo float4 per thread per chunk without expand: 8 * hpb * 16 <= 256 * UH
+template <int K, int ST, int NBW, bool EXP>
 __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -192,12 +198,12 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     const int c_begin = si * a.cpw;
     const int c_end = min(a.nchunk, c_begin + a.cpw);
     const int cv = min(a.coj, a.cout - j * a.coj);  // output channels of this slice
-    const int nf = (a.expand ? CC * (a.cin >> 2) + 8 : 0) + 8 * K * K + 8 + 8 * cv;
+    const int nf = (EXP ? CC * (a.cin >> 2) + 8 : 0) + 8 * K * K + 8 + 8 * cv;
     const int P = a.th * a.tw;
     const int nblk = a.pb * a.ob;
     const int hrows = a.hpb * 16;
 
-    const IrLds L = ir_lds(a.hpb, a.xs, a.expand, K, a.pb, a.ob);
+    const IrLds L = ir_lds(a.hpb, a.xs, EXP, K, a.pb, a.ob);
     float* Xs = lds + L.x;
     float* Ws = lds + L.w;
     const float* Bes = lds + L.be;
@@ -237,7 +243,35 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         for (int t = 0; t < 8; ++t)
             if (xd[t] >= 0) *reinterpret_cast<f4v*>(Xs + xd[t]) = xv[t];
     };
-    load_x(tid);
+    // without expand: the chunk's 32 channels of the halo, 8 float4 per halo row
+    f4v hq[UH];
+    auto load_h = [&](int ch) {
+#pragma unroll
+        for (int u = 0; u < UH; ++u) {
+            const int e = tid + 256 * u;
+            const int r = e >> 3, c = ch * CC + 4 * (e & 7);
+            const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+            const int iy = iy0 + hy, ix = ix0 + hx;
+            const bool in = (r < a.hp) & (c < a.cin) & ((unsigned)iy < (unsigned)a.h) &
+                            ((unsigned)ix < (unsigned)a.w_);
+            hq[u] = ld16(xr, in ? (unsigned)((iy * a.w_ + ix) * a.cin + c) * 4u : kOob);
+        }
+    };
+    auto store_h = [&]() {
+#pragma unroll
+        for (int u = 0; u < UH; ++u) {
+            const int e = tid + 256 * u;
+            if (e < hrows * 8) {
+                float* d = Es + (e >> 3) * ES + 4 * (e & 7);  // rows 33 floats apart
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = hq[u][i];
+            }
+        }
+    };
+    if (EXP)
+        load_x(tid);
+    else if (c_begin < c_end)
+        load_h(c_begin);
 
     // this thread's share of every chunk's weights, and the first chunk's loads
     int goff[NPF], meta[NPF];
@@ -251,19 +285,21 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         buffer_rsrc(a.w, a.w_wd + (int64_t)(K * K + 1 + a.cout) * a.ce + a.cout);
     fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
 
-    store_x();
-    for (int e0 = tid + 2048; e0 < xtotal; e0 += 2048) {  // patches of more than 2048 float4
-        load_x(e0);
+    if (EXP) {
         store_x();
-    }
-    for (int r = tid; r < hrows; r += 256) {
-        const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
-        const int iy = iy0 + hy, ix = ix0 + hx;
-        hvalid[r] = r < a.hp && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_;
+        for (int e0 = tid + 2048; e0 < xtotal; e0 += 2048) {  // patches of more than 2048 float4
+            load_x(e0);
+            store_x();
+        }
+        for (int r = tid; r < hrows; r += 256) {
+            const int hy = udiv(r, a.m_hw), hx = r - hy * a.hw;
+            const int iy = iy0 + hy, ix = ix0 + hx;
+            hvalid[r] = r < a.hp && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w_;
+        }
     }
     // never written by the chunk staging: We padding columns, Wp rows past this slice and
     // the depthwise rows past the tile's pixels (read by the projection as zeros)
-    if (a.expand && a.cin16 > a.cin) {
+    if (EXP && a.cin16 > a.cin) {
         const int pc = a.cin16 - a.cin;
         for (int e = tid; e < CC * pc; e += 256) Ws[(e / pc) * a.xs + a.cin + e % pc] = 0.f;
     }
@@ -279,12 +315,16 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     for (int ch = c_begin; ch < c_end; ++ch) {
         __syncthreads();  // the previous chunk's readers are done with its weights, E and D
         put_weights<0>(pf, lds, meta, tid, nf);
+        if (!EXP) {
+            store_h();
+            if (ch + 1 < c_end) load_h(ch + 1);
+        }
         if (ch + 1 < c_end)  // the next chunk's weights load while this one computes
             fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, ch + 1);
         __syncthreads();
         const int c0 = ch * CC;
         const bool half = c0 + 16 >= a.ce;  // a 16-channel last chunk: one column block
-        if (a.expand) {
+        if (EXP) {
             // E[halo pixel][32 channels]: lane group g sums the K quarter [g*Q, g*Q + Q) of
             // cin16, so each lane reads 16 contiguous bytes of its row per 4 MFMA steps; the
             // row block's x reads serve both column blocks, and the next step's operands are
@@ -344,8 +384,8 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
             // depthwise, one output row of the tile per thread: the K x K window slides
             // along the row in registers (ST new columns per pixel); taps bias first, then
             // row by row as the reference sums them
-            const float* src = a.expand ? Es + dc : Xs + c0 + dc;
-            const int rs = a.expand ? ES : a.xs;
+            const float* src = Es + dc;
+            const int rs = ES;
             const ActClamp act_d(a.act_d);
             float wk[K * K];
 #pragma unroll
@@ -539,6 +579,7 @@ int row_stride(int c16) { return c16 + (36 - c16 % 32) % 32; }
 struct IrGeom {
     int tiles_y, tiles_x, tiles, hh, hw, hp, hpb, cin16, xs, nchunk, cpw, S, J, coj, ob, pb;
     int nblk, nbw, nf_max, lds_floats;
+    bool expand;
 };
 
 IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
@@ -564,11 +605,13 @@ IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
     g.nbw = ceil_div(g.nblk, 4);
     g.nf_max = (sh.expand ? CC * (sh.cin / 4) + 8 : 0) + 8 * sh.k * sh.k + 8 + 8 * g.coj;
     g.lds_floats = ir_lds(g.hpb, g.xs, sh.expand, sh.k, g.pb, g.ob).total;
+    g.expand = sh.expand != 0;
     return g;
 }
 
 bool geometry_ok(const IrGeom& g) {
     return g.lds_floats * 4 <= kMaxLds && g.nbw <= 20 && g.nf_max <= 256 * NPF &&
+           (g.expand || g.hpb * 16 * 8 <= 256 * UH) &&  // the halo chunk's float4 per thread
            (int64_t)g.S * g.nblk * 1024 < (1ll << 31) &&
            // the kernel's multiply-high divisions of the workgroup id stay exact
            (int64_t)g.tiles * g.J * g.S *
@@ -755,22 +798,27 @@ int parse(const int32_t* q, size_t n, IrShape& sh) {
     return SHP_OK;
 }
 
-template <int K, int ST, int NBW>
+template <int K, int ST, int NBW, bool EXP>
 int launch_variant(hipStream_t stream, const IrArgs& a, unsigned grid, size_t lds) {
     if (lds > 64 * 1024)
-        SHP_HIP_CHECK(hipFuncSetAttribute((const void*)ir_kernel<K, ST, NBW>,
+        SHP_HIP_CHECK(hipFuncSetAttribute((const void*)ir_kernel<K, ST, NBW, EXP>,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((ir_kernel<K, ST, NBW>), dim3(grid), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((ir_kernel<K, ST, NBW, EXP>), dim3(grid), dim3(256), lds, stream, a);
     SHP_HIP_CHECK(hipGetLastError());
     return SHP_OK;
 }
 
+template <int K, int ST, bool EXP>
+int launch_nbw_e(hipStream_t stream, const IrArgs& a, int nbw, unsigned grid, size_t lds) {
+    if (nbw <= 2) return launch_variant<K, ST, 2, EXP>(stream, a, grid, lds);
+    if (nbw <= 4) return launch_variant<K, ST, 4, EXP>(stream, a, grid, lds);
+    if (nbw <= 8) return launch_variant<K, ST, 8, EXP>(stream, a, grid, lds);
+    return launch_variant<K, ST, 20, EXP>(stream, a, grid, lds);
+}
 template <int K, int ST>
 int launch_nbw(hipStream_t stream, const IrArgs& a, int nbw, unsigned grid, size_t lds) {
-    if (nbw <= 2) return launch_variant<K, ST, 2>(stream, a, grid, lds);
-    if (nbw <= 4) return launch_variant<K, ST, 4>(stream, a, grid, lds);
-    if (nbw <= 8) return launch_variant<K, ST, 8>(stream, a, grid, lds);
-    return launch_variant<K, ST, 20>(stream, a, grid, lds);
+    return a.expand ? launch_nbw_e<K, ST, true>(stream, a, nbw, grid, lds)
+                    : launch_nbw_e<K, ST, false>(stream, a, nbw, grid, lds);
 }
 
 int launch_ir(const shp::Launch& l) {

@@ -69,6 +69,10 @@ CASES = [  # (label, n, cin, h, w, ce, cout, k, s, expand, residual)
     ("effnet_block11_b2", 2, 112, 14, 14, 672, 192, 5, 2, True, False),
     ("odd_s2", 3, 20, 13, 11, 48, 28, 3, 2, True, False),
     ("odd_k5_res", 2, 36, 10, 9, 64, 36, 5, 1, True, True),
+    # without expand, many input channels (staged 32 at a time over the halo)
+    ("effnet_block12_dwproj_b2", 2, 1152, 7, 7, 1152, 192, 5, 1, False, False),
+    ("effnet_block9_dwproj_b2", 2, 672, 14, 14, 672, 112, 5, 1, False, False),
+    ("dwproj_s2_odd", 3, 48, 9, 11, 48, 24, 3, 2, False, False),
 ]
 
 
@@ -88,7 +92,7 @@ FORCED = [  # (th, tw, expanded-channel splits, output-channel splits)
 
 
 @pytest.mark.parametrize("plan", FORCED, ids=[f"t{a}x{b}_s{c}_j{d}" for a, b, c, d in FORCED])
-@pytest.mark.parametrize("case", [CASES[2], CASES[9], CASES[10]], ids=lambda c: c[0])
+@pytest.mark.parametrize("case", [CASES[2], CASES[9], CASES[10], CASES[13]], ids=lambda c: c[0])
 def test_forced_plans(ctx, orc, case, plan):
     label, n, cin, h, w, ce, cout, k, s, expand, res = case
     th, tw, S, J = plan

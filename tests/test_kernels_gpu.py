@@ -673,8 +673,9 @@ def test_conv2d_reference_and_nhwc(ctx, orc, n, ic, hw, oc, k, s, pad):
     (8, 3, 224, 224, 32, 2, "relu6", False),
     (2, 1, 17, 13, 16, 1, "relu", True),
     (3, 4, 9, 11, 8, 2, None, False),
-    (2, 2, 10, 7, 24, 1, "relu6", True)],
-    ids=["stem-b1", "stem-b8", "ic1-res", "ic4-odd", "ic2-res"])
+    (2, 2, 10, 7, 24, 1, "relu6", True),
+    (4, 2, 160, 160, 40, 1, "relu", False)],  # four channel groups per lane, five groups
+    ids=["stem-b1", "stem-b8", "ic1-res", "ic4-odd", "ic2-res", "ic2-wide"])
 def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, res):
     """3x3 conv2d_nhwc with 1-4 input channels (SAME padding) runs the direct kernel (one
     thread: 8 output channels of one pixel, taps in the padding read as zeros): against the
