@@ -684,6 +684,11 @@ const TunedBlock kTunedBlocks[] = {
     {8, 112, 14, 14, 672, 192, 5, 2, 1, 7, 2, 8, 1, true},    // block11: 28.0 / 28.8
     {8, 192, 7, 7, 1152, 192, 5, 1, 1, 7, 4, 8, 2, false},    // block12-14: 45.6 / 29.7
     {8, 192, 7, 7, 1152, 320, 3, 1, 1, 7, 4, 8, 2, false},    // block15: 42.7 / 27.8
+    // EfficientNet-Lite0 batch 8, the blocks above that do not fuse whole: depthwise +
+    // projection as one launch after the expand GEMM (us: one launch / two launches)
+    {8, 672, 14, 14, 672, 112, 5, 1, 0, 8, 2, 4, 1, true},    // block9-10: 20.7 / 22.9
+    {8, 1152, 7, 7, 1152, 192, 5, 1, 0, 7, 2, 8, 2, true},    // block12-14: 19.0 / 19.6
+    {8, 1152, 7, 7, 1152, 320, 3, 1, 0, 7, 4, 8, 4, false},   // block15: 23.5 / 17.9
 };
 
 const TunedBlock* tuned_block(const IrShape& sh) {

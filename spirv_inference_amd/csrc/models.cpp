@@ -310,7 +310,7 @@ std::vector<int32_t> block_push(const Act4& x, int expand, int k, int s, int cou
 // One MBConv block as a single inverted_residual_nhwc launch: the three operators' weight
 // tensors packed back to back in one tensor and filled in the same order with the same
 // distributions (so the weights equal those of the three-operator graph of the same seed).
-Act4 tfl_block(Model& m, Act4 x, int expand, int k, int s, int cout, bool residual,
+Act4 tfl_block(Model& m, Act4 x, int expand, int k, int s, int cout, int residual,
                const char* label) {
     const int ce = expand != 1 ? x.c * expand : x.c;
     int oh = (x.h + s - 1) / s, ow = (x.w + s - 1) / s;
@@ -328,8 +328,8 @@ Act4 tfl_block(Model& m, Act4 x, int expand, int k, int s, int cout, bool residu
     m.weight_bytes += (double)(ne + nd + np) * 4.0;
     int y = m.tensor((uint64_t)x.n * oh * ow * cout);
     const int64_t total = (int64_t)x.n * oh * ow * cout;
-    m.op("inverted_residual_nhwc", x.t, w, y, block_push(x, expand, k, s, cout), -1,
-         residual ? x.t : -1, SHP_ACT_NONE, 0.0f, label);
+    m.op("inverted_residual_nhwc", x.t, w, y, block_push(x, expand, k, s, cout), -1, residual,
+         SHP_ACT_NONE, 0.0f, label);
     if (expand != 1) m.flops += 2.0 * (double)x.n * x.h * x.w * x.c * ce;
     m.flops += 2.0 * (double)x.n * oh * ow * ce * k * k + 2.0 * (double)total * ce;
     return Act4{y, x.n, oh, ow, cout};
@@ -370,18 +370,26 @@ int tfl_net(Model& m, int batch, const MBConv* cfg, int ncfg, int stem_c) {
             if (fuse > 0 || (fuse == 0 && block_fusion_pays(bp.data(), bp.size()))) {
                 std::snprintf(label, sizeof label, "block%d_mbconv", bi);
                 x = tfl_block(m, x, cfg[i].expand, cfg[i].k, s, cfg[i].c,
-                              s == 1 && x.c == cfg[i].c, label);
+                              s == 1 && x.c == cfg[i].c ? x.t : -1, label);
                 continue;
             }
             Act4 in_x = x;
             Act4 h = x;
+            bool res = s == 1 && in_x.c == cfg[i].c;
             if (cfg[i].expand != 1) {
                 std::snprintf(label, sizeof label, "block%d_expand", bi);
                 h = tfl_conv(m, x, x.c * cfg[i].expand, 1, 1, SHP_ACT_RELU6, -1, label);
+                // the depthwise and the projection as one launch where that pays (the
+                // expanded tensor as the input; its weights fill as the two operators')
+                const std::vector<int32_t> dp = block_push(h, 1, cfg[i].k, s, cfg[i].c);
+                if (fuse == 0 && block_fusion_pays(dp.data(), dp.size())) {
+                    std::snprintf(label, sizeof label, "block%d_dwproj", bi);
+                    x = tfl_block(m, h, 1, cfg[i].k, s, cfg[i].c, res ? in_x.t : -1, label);
+                    continue;
+                }
             }
             std::snprintf(label, sizeof label, "block%d_depthwise", bi);
             h = tfl_depthwise(m, h, cfg[i].k, s, SHP_ACT_RELU6, label);
-            bool res = s == 1 && in_x.c == cfg[i].c;
             std::snprintf(label, sizeof label, "block%d_project", bi);
             x = tfl_conv(m, h, cfg[i].c, 1, 1, SHP_ACT_NONE, res ? in_x.t : -1, label);
         }

@@ -600,7 +600,8 @@ class TfliteExecutor:
     dispatches nothing.  An inverted-residual chain, [1x1 CONV_2D] -> DEPTHWISE_CONV_2D ->
     1x1 CONV_2D [-> residual ADD], whose intermediates nothing else reads, runs as one
     inverted_residual_nhwc launch at the projection where the library expects that to beat
-    the three launches (shp_block_plan); fuse_blocks=True fuses every chain the kernel takes,
+    the three launches (shp_block_plan), else, where that pays, the expand as its own launch
+    and the depthwise + projection as one; fuse_blocks=True fuses every chain the kernel takes,
     False none.  A 1x1 CONV_2D read only by a global pool (the classifier head) runs as one
     conv1x1_gap_nhwc launch unless fuse_blocks is False.  Anything else raises, like the
     reference's scheduler.
@@ -739,9 +740,17 @@ class TfliteExecutor:
                 ei = None
             blk = {"expand": ei, "dw": dw.index, "src": src}
             plan = self._block_plan(ops[pi], blk)
-            if plan is None or (only_if_faster and not plan[7]):
-                continue
-            out[pi] = blk
+            if plan is not None and plan[7]:
+                out[pi] = blk
+            elif ei is not None and only_if_faster:
+                # the expand as its own launch, the depthwise and projection as one where
+                # that pays (as the model graphs decide)
+                sub = {"expand": None, "dw": dw.index, "src": dw.inputs[0]}
+                plan = self._block_plan(ops[pi], sub)
+                if plan is not None and plan[7]:
+                    out[pi] = sub
+            elif plan is not None and not only_if_faster:
+                out[pi] = blk
         return out
 
     def _find_heads(self) -> Dict[int, int]:
@@ -1218,7 +1227,10 @@ def model_to_tflite(m, description: str = "") -> bytes:
             n, cin, h, w_, ce, cout, oh, ow, kk, s, pt, pl, expand, act_e, act_d = q[:15]
             packed, o = host(op.in1), 0
             x = model_input(op.in0, [n, h, w_, cin])
-            base = op.label[:-len("_mbconv")] if op.label.endswith("_mbconv") else op.label
+            base = op.label
+            for suffix in ("_mbconv", "_dwproj"):
+                if base.endswith(suffix):
+                    base = base[:-len(suffix)]
             if expand:
                 x = conv(f"{base}_expand", x, n, cin, h, w_, ce, 1, 1, True,
                          packed[:ce * cin], packed[ce * cin:ce * cin + ce], _ACT_TO_TFL[act_e])
