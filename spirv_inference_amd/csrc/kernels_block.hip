@@ -1117,9 +1117,9 @@ int launch_conv1x1_gap(const shp::Launch& l) {
     if ((int64_t)n * cblk >= (1ll << 31))
         return shp::fail(SHP_ERR_SHAPE, "conv1x1_gap_nhwc: grid too large");
     if (hw <= 64 && cin <= 512) {
-        // two column blocks per workgroup once that still leaves >= 512 workgroups
+        // two column blocks per workgroup once that still leaves >= 256 workgroups
         const int cb2 = (cout + 31) / 32;
-        if ((int64_t)n * cb2 >= 512) {
+        if ((int64_t)n * cb2 >= 256) {
             hipLaunchKernelGGL((conv1x1_gap_small_kernel<2>), dim3((unsigned)(n * cb2)), dim3(256),
                                0, l.stream, (const float*)l.in0, (const float*)l.in1,
                                (float*)l.out, cin, (int)hw, cout, cb2, l.epi->act, l.epi->alpha);

@@ -1515,45 +1515,70 @@ __global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restr
                                                             int K, const float* __restrict__ bias,
                                                             int act, float alpha) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [M][K]
+    const int lane = threadIdx.x & 63;
+    const int n0 = blockIdx.x * 8 + 2 * (threadIdx.x >> 6);
+    const bool col = n0 < N;
+    const bool two = n0 + 1 < N;
+    const float* w0 = w + (int64_t)(col ? n0 : 0) * K;
+    const float* w1 = two ? w0 + K : w0;
+    // K <= 2048: all of this lane's weights of both columns are loaded first, so their HBM
+    // round trip overlaps the staging of x (longer K loops four K steps at a time below)
+    constexpr int KR = 8;
+    const bool resident = K <= 256 * KR;
+    f4v u[KR], v[KR];
+    if (resident && col) {
+#pragma unroll
+        for (int j = 0; j < KR; ++j) {
+            const int k = lane * 4 + 256 * j;
+            if (k < K) {
+                u[j] = *reinterpret_cast<const f4v*>(w0 + k);
+                v[j] = *reinterpret_cast<const f4v*>(w1 + k);
+            }
+        }
+    }
     for (int i0 = threadIdx.x * 4; i0 < M * K; i0 += 8192) {  // 8 loads in flight per thread
         f4v t[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (i0 + 1024 * u < M * K) t[u] = *reinterpret_cast<const f4v*>(x + i0 + 1024 * u);
+        for (int q = 0; q < 8; ++q)
+            if (i0 + 1024 * q < M * K) t[q] = *reinterpret_cast<const f4v*>(x + i0 + 1024 * q);
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (i0 + 1024 * u < M * K) *reinterpret_cast<f4v*>(xs + i0 + 1024 * u) = t[u];
+        for (int q = 0; q < 8; ++q)
+            if (i0 + 1024 * q < M * K) *reinterpret_cast<f4v*>(xs + i0 + 1024 * q) = t[q];
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int n0 = blockIdx.x * 8 + 2 * (threadIdx.x >> 6);
-    if (n0 >= N) return;
-    const bool two = n0 + 1 < N;
-    const float* w0 = w + (int64_t)n0 * K;
-    const float* w1 = two ? w0 + K : w0;
+    if (!col) return;
     float a0[MR], a1[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) a0[m] = a1[m] = 0.0f;
-    for (int k0 = lane * 4; k0 < K; k0 += 1024) {  // four K steps' weights in flight
-        f4v u[4], v[4];
+    auto step = [&](const f4v& uj, const f4v& vj, int k) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (k0 + 256 * j < K) {
-                u[j] = *reinterpret_cast<const f4v*>(w0 + k0 + 256 * j);
-                v[j] = *reinterpret_cast<const f4v*>(w1 + k0 + 256 * j);
+        for (int m = 0; m < MR; ++m) {
+            if (m < M) {
+                const f4v xv = *reinterpret_cast<const f4v*>(xs + m * K + k);
+                a0[m] += uj.x * xv.x + uj.y * xv.y + uj.z * xv.z + uj.w * xv.w;
+                a1[m] += vj.x * xv.x + vj.y * xv.y + vj.z * xv.z + vj.w * xv.w;
             }
         }
+    };
+    if (resident) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = k0 + 256 * j;
+        for (int j = 0; j < KR; ++j) {
+            const int k = lane * 4 + 256 * j;
+            if (k < K) step(u[j], v[j], k);
+        }
+    } else {
+        for (int k0 = lane * 4; k0 < K; k0 += 1024) {  // four K steps' weights in flight
+            f4v uu[4], vv[4];
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                if (m < M && k < K) {
-                    const f4v xv = *reinterpret_cast<const f4v*>(xs + m * K + k);
-                    a0[m] += u[j].x * xv.x + u[j].y * xv.y + u[j].z * xv.z + u[j].w * xv.w;
-                    a1[m] += v[j].x * xv.x + v[j].y * xv.y + v[j].z * xv.z + v[j].w * xv.w;
+            for (int jj = 0; jj < 4; ++jj) {
+                if (k0 + 256 * jj < K) {
+                    uu[jj] = *reinterpret_cast<const f4v*>(w0 + k0 + 256 * jj);
+                    vv[jj] = *reinterpret_cast<const f4v*>(w1 + k0 + 256 * jj);
                 }
             }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                if (k0 + 256 * jj < K) step(uu[jj], vv[jj], k0 + 256 * jj);
         }
     }
 #pragma unroll
