@@ -47,6 +47,9 @@ struct GemmTune {
     // conv2d_nhwc with <= 4 input channels: the direct kernel where it fits (0) or the
     // implicit-GEMM kernels (-1)
     int conv_direct = 0;
+    // 1x1 conv2d_nhwc with K <= 256: the register-resident small-product kernel where the 64x64
+    // tiles would not fill the GPU (0), wherever it takes the shape (1), never (-1)
+    int small = 0;
 };
 
 // Everything a launcher needs: the three bindings, the push vector and the epilogue.

@@ -1603,6 +1603,65 @@ __global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restr
     }
 }
 
+// ---- small products (small_gemm_kernel): C[M][N] = A[M][K] B[N][K]^T + bias (+ residual),
+// activation, for K <= 256 and grids the 64x64 tiles would leave half empty (the 1x1
+// expand convolutions of EfficientNet-Lite0 at batch 8: M 392-1,568, N 480-1,152, K 80-192).
+// A workgroup owns a 32x32 output tile and each wavefront one 16x16 block of it on
+// v_mfma_f32_16x16x4_f32.  Every operand of the whole K goes into registers at once (lane
+// group g reads the K quarter [4g, 4g + 4) of each 16-wide K step, 16 contiguous bytes of its
+// row of A or B; K past the end reads zeros through the buffer range), so the product waits
+// for one round trip instead of one per K tile; two accumulators take alternate K steps.
+typedef float floatx4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ floatx4s mfma4_16(f4v a, f4v b, floatx4s c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+}
+constexpr int kSmallKc = 16;  // 16-wide K steps a lane holds: K <= 256
+__global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict__ A,
+                                                         const float* __restrict__ B,
+                                                         float* __restrict__ C, int M, int N,
+                                                         int K, int tiles_n,
+                                                         const float* __restrict__ bias,
+                                                         const float* __restrict__ res, int act,
+                                                         float alpha) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, li = lane & 15;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+    const int m0 = tm * 32 + (wave >> 1) * 16, n0 = tn * 32 + (wave & 1) * 16;
+    const int row = m0 + li, col = n0 + li;
+    const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(A, (int64_t)M * K);
+    const __amdgpu_buffer_rsrc_t br = buffer_rsrc(B, (int64_t)N * K);
+    const unsigned arow = (unsigned)(row * K) * 4u, brow = (unsigned)(col * K) * 4u;
+    f4v a[kSmallKc], b[kSmallKc];
+#pragma unroll
+    for (int c = 0; c < kSmallKc; ++c) {
+        const int k = 16 * c + 4 * g;
+        const bool kok = k < K;
+        a[c] = buffer_load4(ar, kok && row < M ? arow + 4u * k : kOobOffset, 0u);
+        b[c] = buffer_load4(br, kok && col < N ? brow + 4u * k : kOobOffset, 0u);
+    }
+    floatx4s e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
+#pragma unroll
+    for (int c = 0; c < kSmallKc; c += 2) {
+        if (16 * c < K) e0 = mfma4_16(a[c], b[c], e0);
+        if (16 * c + 16 < K) e1 = mfma4_16(a[c + 1], b[c + 1], e1);
+    }
+    if (col >= N) return;
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // accumulator r: row 4g + r of the block, column li
+        const int m = m0 + 4 * g + r;
+        if (m < M) {
+            const int64_t o = (int64_t)m * N + col;
+            float v = e0[r] + e1[r] + bv;
+            if (res) v += res[o];
+            C[o] = shpd::apply_act(v, act, alpha);
+        }
+    }
+}
+
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
     int bm, bn, bk;
@@ -2347,6 +2406,24 @@ int conv2d_common(const shp::Launch& l, bool nhwc) {
     if (nhwc && q[1] <= 4 && !(l.tune && l.tune->conv_direct < 0)) {
         rc = shp::conv_nhwc_direct(l);
         if (rc != SHP_ERR_UNSUPPORTED) return rc;
+    }
+    // 1x1 stride-1 unpadded NHWC convolutions are plain [M][K] x [N][K]^T products: the
+    // register-resident small kernel where K <= 256 and the 64x64 tiles would not fill the GPU
+    const int small = l.tune ? l.tune->small : 0;
+    if (nhwc && small >= 0 && q[7] == 1 && q[8] == 1 && q[9] == 1 && q[10] == 1 && q[12] == 0 &&
+        q[13] == 0 && q[5] == q[2] && q[6] == q[3] && p.K % 4 == 0 && p.K <= 16 * kSmallKc &&
+        al16(p.a) && al16(p.b) && (int64_t)p.M * p.K * 4 < (1ll << 31) &&
+        (int64_t)p.N * p.K * 4 < (1ll << 31) &&
+        (small > 0 || (int64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) < 512)) {
+        const int tiles_n = (p.N + 31) / 32;
+        const int64_t grid = (int64_t)((p.M + 31) / 32) * tiles_n;
+        if (grid < (1ll << 31)) {
+            hipLaunchKernelGGL(small_gemm_kernel, dim3((unsigned)grid), dim3(256), 0, l.stream,
+                               p.a, p.b, p.c, p.M, p.N, p.K, tiles_n, p.bias, p.residual,
+                               p.act, p.alpha);
+            SHP_HIP_CHECK(hipGetLastError());
+            return SHP_OK;
+        }
     }
     int bm = (p.K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
     if (nhwc) {

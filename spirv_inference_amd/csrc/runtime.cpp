@@ -325,7 +325,8 @@ int shp_workspace_info(shp_ctx* ctx, void** dptr, uint64_t* bytes) {
 // automatic choice): gemm_tile, gemm_bk, gemm_splits, gemm_dma, gemm_pg, gemm_table, gemm_bl,
 // gemm_sk, gemm_stem, gemm_group, dw_tile; the fused block's ir_th, ir_tw, ir_splits,
 // ir_cout_splits and the model graphs' ir_fuse; conv_direct (-1: small-channel 3x3
-// conv2d_nhwc on the implicit GEMM instead of the direct kernel).
+// conv2d_nhwc on the implicit GEMM instead of the direct kernel); gemm_small (1x1 conv2d_nhwc
+// with K <= 256 on the register-resident small kernel: 1 wherever it fits, -1 never).
 int shp_tune(shp_ctx* ctx, const char* key, int value) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_tune: null ctx");
     shp::GemmTune& t = reinterpret_cast<Ctx*>(ctx)->tune;
@@ -347,6 +348,7 @@ int shp_tune(shp_ctx* ctx, const char* key, int value) {
     else if (k == "ir_cout_splits") t.ir_j = value;
     else if (k == "ir_fuse") t.ir_fuse = value;
     else if (k == "conv_direct") t.conv_direct = value;
+    else if (k == "gemm_small") t.small = value;
     else return fail(SHP_ERR_INVALID, "shp_tune: unknown key '" + k + "'");
     return SHP_OK;
 }

@@ -706,6 +706,38 @@ def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, re
         assert not np.array_equal(y, y0), "the direct kernel did not run"
 
 
+@pytest.mark.parametrize("n,ic,h,w,oc,act,res", [
+    (8, 112, 14, 14, 672, "relu6", False),   # EfficientNet-Lite0 b8 block 9 expand
+    (8, 192, 7, 7, 1152, "relu6", False),    # block 12 expand
+    (3, 20, 5, 7, 36, None, True),           # partial 32x32 tiles, residual
+    (2, 4, 9, 9, 8, "relu", False),          # one K step
+    (1, 256, 6, 6, 40, None, True)],         # K at the register limit
+    ids=["effnet-b9-expand", "effnet-b12-expand", "odd-res", "k4", "k256"])
+def test_conv2d_nhwc_1x1_small_kernel(ctx, orc, n, ic, h, w, oc, act, res):
+    """1x1 conv2d_nhwc with K <= 256 on the register-resident small-product kernel (32x32
+    tiles, all of K loaded at once): against the oracle, and against the tiled GEMM with the
+    small kernel switched off (both agree with the oracle; their K orders differ, so some
+    outputs differ in the last bits, which shows the small kernel ran)."""
+    total = n * h * w * oc
+    push = [n, ic, h, w, oc, h, w, 1, 1, 1, 1, 1, 0, 0, total]
+    wt = np.concatenate([rnd(oc * ic, scale=float(np.sqrt(2.0 / ic))), rnd(oc, scale=0.1)])
+    x = rnd(n, h, w, ic)
+    kw = {"act": act} if act else {}
+    if res:
+        kw["residual"] = rnd(total)
+    try:
+        _tune(ctx, "gemm_small", 1)
+        y, r = both(ctx, orc, "conv2d_nhwc", x, wt, total, push, **kw)
+        _tune(ctx, "gemm_small", -1)
+        y0 = hip(ctx, "conv2d_nhwc", x, wt, total, push, **kw)
+    finally:
+        _tune(ctx, "gemm_small", 0)
+    assert_close(y, r, 1e-4, 1e-4, f"small 1x1 conv {push[:7]}")
+    assert_close(y0, r, 1e-4, 1e-4, f"tiled 1x1 conv {push[:7]}")
+    if total >= 4096:
+        assert not np.array_equal(y, y0), "the small kernel did not run"
+
+
 @pytest.mark.parametrize("b,k,n", [(1, 1280, 1000), (8, 1280, 1000), (32, 2048, 1000),
                                    (3, 37, 5), (5, 64, 13), (2, 4096, 9)])
 def test_fully_connected(ctx, orc, b, k, n):
