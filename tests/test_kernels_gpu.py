@@ -710,14 +710,19 @@ def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, re
     (8, 112, 14, 14, 672, "relu6", False),   # EfficientNet-Lite0 b8 block 9 expand
     (8, 192, 7, 7, 1152, "relu6", False),    # block 12 expand
     (3, 20, 5, 7, 36, None, True),           # partial 32x32 tiles, residual
-    (2, 4, 9, 9, 8, "relu", False),          # one K step
-    (1, 256, 6, 6, 40, None, True)],         # K at the register limit
-    ids=["effnet-b9-expand", "effnet-b12-expand", "odd-res", "k4", "k256"])
+    (2, 4, 9, 9, 8, "relu", False),          # one K quarter
+    (2, 24, 11, 13, 144, "relu6", False),    # two chunks, the second partly past K
+    (1, 80, 14, 14, 480, "relu6", True),     # five chunks of the eight-chunk variant
+    (1, 240, 3, 5, 70, None, True),          # fifteen chunks
+    (1, 256, 6, 6, 40, None, True)],         # K at the limit (LDS beyond 64 KiB)
+    ids=["effnet-b9-expand", "effnet-b12-expand", "odd-res", "k4", "k24", "k80", "k240",
+         "k256"])
 def test_conv2d_nhwc_1x1_small_kernel(ctx, orc, n, ic, h, w, oc, act, res):
-    """1x1 conv2d_nhwc with K <= 256 on the register-resident small-product kernel (32x32
-    tiles, all of K loaded at once): against the oracle, and against the tiled GEMM with the
-    small kernel switched off (both agree with the oracle; their K orders differ, so some
-    outputs differ in the last bits, which shows the small kernel ran)."""
+    """1x1 conv2d_nhwc with K <= 256 on the small-product kernel (32x32 tiles, operands
+    staged through LDS in 16-wide K chunks, each multiplied as it lands): against the oracle,
+    and against the tiled GEMM with the small kernel switched off (both agree with the oracle;
+    their K orders differ, so some outputs differ in the last bits, which shows the small
+    kernel ran)."""
     total = n * h * w * oc
     push = [n, ic, h, w, oc, h, w, 1, 1, 1, 1, 1, 0, 0, total]
     wt = np.concatenate([rnd(oc * ic, scale=float(np.sqrt(2.0 / ic))), rnd(oc, scale=0.1)])
