@@ -1683,6 +1683,65 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
     }
 }
 
+// ---- fully_connected with 2-16 rows (fc_mfma_kernel): y[M][N] = x[M][K] W[N][K]^T + bias
+// (+ residual), activation.  One workgroup of 16 wavefronts owns 16 output columns, and
+// wavefront w takes the w-th sixteenth of K's 16-wide chunks on v_mfma_f32_16x16x4_f32 (rows
+// past M, columns past N and K past the end read zeros through the buffer range), with all its
+// loads issued before the first MFMA.  The sixteen partial 16x16 tiles are summed in LDS in
+// wavefront order.  The weights are the traffic (5 MB at K = 1,280, N = 1,000): ~1,000
+// wavefronts stream them once, where the wavefront-per-column kernels gave each wavefront a
+// whole 5 KB column plus the M activation rows (EfficientNet-Lite0's classifier at batch 8:
+// 12.6 us for one wavefront per column, 6.0 us here, graph-replayed with the weights cold).
+constexpr int kFcWaves = 16;
+template <int CPW>
+__global__ __launch_bounds__(kFcWaves * 64) void fc_mfma_kernel(
+    const float* __restrict__ X, const float* __restrict__ W, float* __restrict__ Y, int M, int N,
+    int K, const float* __restrict__ bias, const float* __restrict__ res, int act, float alpha) {
+    __shared__ float red[kFcWaves * 4 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, li = lane & 15;
+    const int n0 = blockIdx.x * 16;
+    const int kc = (K + 15) >> 4, cpw = (kc + kFcWaves - 1) / kFcWaves, c0 = wave * cpw;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, (int64_t)M * K);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (int64_t)N * K);
+    const bool xok = li < M, wok = n0 + li < N;
+    const unsigned xb = (unsigned)(li * K + 4 * g) * 4u;
+    const unsigned wb = (unsigned)((n0 + li) * K + 4 * g) * 4u;
+    f4v a[CPW], b[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        const bool ok = j < cpw && 16 * (c0 + j) + 4 * g < K;
+        b[j] = buffer_load4(wr, ok && wok ? wb + 64u * (c0 + j) : kOobOffset, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        const bool ok = j < cpw && 16 * (c0 + j) + 4 * g < K;
+        a[j] = buffer_load4(xr, ok && xok ? xb + 64u * (c0 + j) : kOobOffset, 0u);
+    }
+    floatx4s e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        if (j & 1) e1 = mfma4_16(a[j], b[j], e1);
+        else e0 = mfma4_16(a[j], b[j], e0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 4 + r) * 64 + lane] = e0[r] + e1[r];
+    __syncthreads();
+    if (tid < 256) {  // output row tid / 16, column n0 + tid % 16: lane (row / 4) * 16 + col, r = row % 4
+        const int row = tid >> 4, col = tid & 15;
+        const int l = (row >> 2) * 16 + col, r = row & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kFcWaves; ++w) v += red[(w * 4 + r) * 64 + l];
+        if (row < M && n0 + col < N) {
+            const int64_t o = (int64_t)row * N + n0 + col;
+            v += bias ? bias[n0 + col] : 0.0f;
+            if (res) v += res[o];
+            Y[o] = shpd::apply_act(v, act, alpha);
+        }
+    }
+}
+
 // ---- host-side dispatch --------------------------------------------------------------
 struct TileCfg {
     int bm, bn, bk;
@@ -2481,6 +2540,20 @@ int launch_fully_connected(const shp::Launch& l) {
     int M = q[0], K = q[1], N = q[2];
     const float* w = (const float*)l.in1;
     const float* bias = w + (int64_t)N * K;
+    const int fcm = l.tune ? l.tune->fc : 0;
+    if (fcm >= 0 && M >= 2 && M <= 16 && K % 4 == 0 && K <= 16 * kFcWaves * 8 && al16(l.in0) &&
+        al16(w) && (int64_t)(N + 16) * K * 4 < (1ll << 31)) {
+        const int cpw = ((K + 15) / 16 + kFcWaves - 1) / kFcWaves;
+        auto kern = cpw <= 1 ? fc_mfma_kernel<1>
+                  : cpw <= 2 ? fc_mfma_kernel<2>
+                  : cpw <= 4 ? fc_mfma_kernel<4>
+                  : cpw <= 5 ? fc_mfma_kernel<5> : fc_mfma_kernel<8>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)((N + 15) / 16)), dim3(kFcWaves * 64), 0,
+                           l.stream, (const float*)l.in0, w, (float*)l.out, M, N, K, bias,
+                           l.epi->residual, l.epi->act, l.epi->alpha);
+        SHP_HIP_CHECK(hipGetLastError());
+        return SHP_OK;
+    }
     if (M <= 8 && !l.epi->residual) {
         unsigned g = (unsigned)((N + 3) / 4);
         if (M <= 1)

@@ -752,6 +752,36 @@ def test_fully_connected(ctx, orc, b, k, n):
     assert_close(y, r, 1e-4, 1e-4, "fc")
 
 
+@pytest.mark.parametrize("m,k,n,act,res", [
+    (8, 1280, 1000, None, False),   # EfficientNet-Lite0 b8 classifier
+    (2, 1280, 1000, "relu", False),
+    (16, 768, 77, None, True),      # 16 rows, column tail, residual
+    (5, 20, 13, "relu6", False),    # fewer chunks than wavefronts
+    (3, 2048, 40, None, False)],    # eight chunks per wavefront
+    ids=["b8-classifier", "m2-relu", "m16-res", "short-k", "k2048"])
+def test_fully_connected_mfma(ctx, orc, m, k, n, act, res):
+    """fully_connected with 2-16 rows on the split-K MFMA kernel: against the oracle, and
+    against the wavefront-per-column / tiled kernels with it switched off (both agree with the
+    oracle; their K orders differ, so some outputs differ in the last bits, which shows the
+    MFMA kernel ran)."""
+    w = np.concatenate([rnd(n * k, scale=float(np.sqrt(1.0 / k))), rnd(n)])
+    x = rnd(m, k)
+    kw = {"act": act} if act else {}
+    if res:
+        kw["residual"] = rnd(m * n)
+    push = [m, k, n, m * n]
+    y, r = both(ctx, orc, "fully_connected", x, w, m * n, push, **kw)
+    try:
+        _tune(ctx, "fc_mfma", -1)
+        y0 = hip(ctx, "fully_connected", x, w, m * n, push, **kw)
+    finally:
+        _tune(ctx, "fc_mfma", 0)
+    assert_close(y, r, 1e-4, 1e-4, f"fc mfma {push}")
+    assert_close(y0, r, 1e-4, 1e-4, f"fc other {push}")
+    if m * n >= 2000:
+        assert not np.array_equal(y, y0), "the MFMA kernel did not run"
+
+
 @pytest.mark.parametrize("bt,m,k,n", [(1, 32, 2048, 1000), (96, 128, 64, 128), (96, 128, 128, 64),
                                       (1, 1024, 768, 3072), (2, 33, 17, 65), (1, 64, 2048, 256)])
 def test_dot_batched(ctx, orc, bt, m, k, n):
