@@ -47,8 +47,8 @@ struct GemmTune {
     // conv2d_nhwc with <= 4 input channels: the direct kernel where it fits (0) or the
     // implicit-GEMM kernels (-1)
     int conv_direct = 0;
-    // 1x1 conv2d_nhwc with K <= 256: the small-product kernel where the 64x64 tiles would not
-    // fill the GPU (0), wherever it takes the shape (1), never (-1)
+    // 1x1 conv2d_nhwc: the small-product kernel where the 64x64 tiles would not fill the GPU
+    // (0), wherever it takes the shape (1), with k >= 2 K-splits (k), never (-1)
     int small = 0;
     // fully_connected with 2-16 rows: the split-K MFMA kernel where it takes the shape (0) or
     // the wavefront-per-column and tiled kernels (-1)

@@ -1604,19 +1604,19 @@ __global__ __launch_bounds__(256) void skinny_nt_lds_kernel(const float* __restr
 }
 
 // ---- small products (small_gemm_kernel): C[M][N] = A[M][K] B[N][K]^T + bias (+ residual),
-// activation, for K <= 256 and grids the 64x64 tiles would leave half empty (the 1x1
-// convolutions of MobileNetV2 at batch 1: M 49-12,544, N 16-1,280, K 16-320 where K <= 256;
-// the expand convolutions of EfficientNet-Lite0 at batch 8: M 392-1,568, N 480-1,152).
+// activation, for grids the 64x64 tiles would leave half empty (the 1x1 convolutions of
+// MobileNetV2 at batch 1: M 49-12,544, N 16-1,280, K 16-960; the expand convolutions of
+// EfficientNet-Lite0 at batch 8: M 392-1,568, N 480-1,152, K 80-192).
 // A workgroup owns a 32x32 output tile and each wavefront one 16x16 block of it on
 // v_mfma_f32_16x16x4_f32.  The tile's 64 operand rows (32 of A, 32 of B) are staged through
 // LDS in 16-wide K chunks: thread t owns row t / 4 and K quarter t % 4 of every chunk (16
 // contiguous bytes; K past the end reads zeros through the buffer range), and issues the
-// loads of all chunks at once.  Chunk c is stored to its own LDS slice and multiplied as soon
-// as its load lands, so the MFMAs of early chunks overlap the arrival of later ones (each
-// slice is written once: one barrier per chunk, no reuse hazard); two accumulators take
-// alternate chunks.  Measured at 32x32 against register-resident fragments (each wavefront
-// loading its own rows), all-loads-then-multiply through LDS, and 64-wide tiles: 1.4-1.7x
-// faster on the EfficientNet-Lite0 expand shapes.
+// loads of all its chunks at once.  Chunk c is stored to an LDS slice and multiplied as soon
+// as its load lands, so the MFMAs of early chunks overlap the arrival of later ones; two
+// accumulators take alternate chunks.  Measured at 32x32 against register-resident
+// fragments (each wavefront loading its own rows), all-loads-then-multiply through LDS, and
+// 64-wide tiles: 1.4-1.7x faster on the EfficientNet-Lite0 expand shapes; two 5 KB slices
+// instead of one slice per chunk keep the workgroup's LDS small enough for 8 per CU.
 typedef float floatx4s __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ floatx4s mfma4_16(f4v a, f4v b, floatx4s c) {
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
@@ -1624,10 +1624,17 @@ __device__ __forceinline__ floatx4s mfma4_16(f4v a, f4v b, floatx4s c) {
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
 }
-constexpr int kSmallKc = 16;  // 16-wide K chunks at most: K <= 256
-// LDS floats per staged row for kc chunks (the 4-float pad spreads the 16 rows a fragment
-// read touches over the banks)
-__host__ __device__ constexpr int small_gemm_kp(int kc) { return 16 * kc + 4; }
+constexpr int kSmallKc = 16;        // 16-wide K chunks of one workgroup at most
+constexpr int kSmallMaxSplits = 8;  // K ranges of one tile: K <= 16 * 16 * 8 = 2,048
+// LDS: chunk c goes to slice c % 2 of 64 rows x kSmallRs floats (16 + a 4-float pad that
+// spreads the 16 rows a fragment read touches over the banks); a slice is rewritten two chunks
+// later, after every wavefront has passed the barrier that follows its last read of it
+constexpr int kSmallRs = 20;
+constexpr int kSmallSlice = 64 * kSmallRs;
+// With gridDim.y = S > 1 the workgroups (tile, s) take the s-th of S equal runs of K's
+// chunks, store their partial tiles with device-coherent stores into `part` (S x 256 float4
+// per tile) and count their arrival on the tile's counter; the last arrival sums the partials
+// in split order and applies the epilogue, then clears the counter.
 template <int KC>
 __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict__ A,
                                                          const float* __restrict__ B,
@@ -1635,11 +1642,15 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
                                                          int K, int tiles_n,
                                                          const float* __restrict__ bias,
                                                          const float* __restrict__ res, int act,
-                                                         float alpha) {
-    extern __shared__ float sg_lds[];
+                                                         float alpha, float* __restrict__ part,
+                                                         int* __restrict__ counters) {
+    __shared__ float sg_lds[2 * kSmallSlice];
+    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, li = lane & 15;
-    const int kc = (K + 15) >> 4, kp = small_gemm_kp(kc);
+    const int S = gridDim.y, si = blockIdx.y;
+    const int kc_all = (K + 15) >> 4, cps = (kc_all + S - 1) / S;
+    const int c0 = si * cps, kc = min(cps, kc_all - c0);
     const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
     const int mb = tm * 32, nb = tn * 32;
     const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(A, (int64_t)M * K);
@@ -1648,25 +1659,54 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
     const bool isa = sr < 32;
     const int grow = isa ? mb + sr : nb + sr - 32;
     const bool rok = grow < (isa ? M : N);
-    const unsigned base = (unsigned)(grow * K + 4 * sq) * 4u;
+    const unsigned base = rok ? (unsigned)(grow * K + 16 * c0 + 4 * sq) * 4u : 0u;
     f4v st[KC];
 #pragma unroll
     for (int c = 0; c < KC; ++c)
         st[c] = buffer_load4(isa ? ar : br,
-                             rok && 16 * c + 4 * sq < K ? base + 64u * c : kOobOffset, 0u);
+                             rok && c < kc && 16 * (c0 + c) + 4 * sq < K ? base + 64u * c
+                                                                        : kOobOffset,
+                             0u);
     const int wm = wave >> 1, wn = wave & 1;
-    const float* fa = sg_lds + (wm * 16 + li) * kp + 4 * g;
-    const float* fb = sg_lds + (32 + wn * 16 + li) * kp + 4 * g;
+    const int fa = (wm * 16 + li) * kSmallRs + 4 * g;
+    const int fb = (32 + wn * 16 + li) * kSmallRs + 4 * g;
     floatx4s e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
         if (c < kc) {  // uniform over the workgroup
-            *(f4v*)(sg_lds + sr * kp + 16 * c + 4 * sq) = st[c];
+            float* sl = sg_lds + (c & 1) * kSmallSlice;
+            *(f4v*)(sl + sr * kSmallRs + 4 * sq) = st[c];
             __syncthreads();
-            const f4v af = *(const f4v*)(fa + 16 * c), bf = *(const f4v*)(fb + 16 * c);
+            const f4v af = *(const f4v*)(sl + fa), bf = *(const f4v*)(sl + fb);
             if (c & 1) e1 = mfma4_16(af, bf, e1);
             else e0 = mfma4_16(af, bf, e0);
         }
+    }
+    if (S > 1) {
+        const __amdgpu_buffer_rsrc_t prs =
+            buffer_rsrc(part + (int64_t)blockIdx.x * S * 1024, (int64_t)S * 1024);
+        st_coh16(prs, (unsigned)((si * 256 + tid) * 16),
+                 make_float4(e0[0] + e1[0], e0[1] + e1[1], e0[2] + e1[2], e0[3] + e1[3]));
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial is stored
+        __syncthreads();
+        if (tid == 0)
+            last = __hip_atomic_fetch_add((SHP_GLOBAL int*)(counters + blockIdx.x), 1,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+        __syncthreads();
+        if (!last) return;
+        if (tid == 0)  // every split has arrived: the counter is free for the next launch
+            __hip_atomic_store((SHP_GLOBAL int*)(counters + blockIdx.x), 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        float4 q[kSmallMaxSplits];
+#pragma unroll
+        for (int u = 0; u < kSmallMaxSplits; ++u)
+            if (u < S) q[u] = ld_coh16(prs, (unsigned)((u * 256 + tid) * 16), 0);
+        f4v t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kSmallMaxSplits; ++u)
+            if (u < S) t += f4v{q[u].x, q[u].y, q[u].z, q[u].w};
+        e0 = floatx4s{t.x, t.y, t.z, t.w};
+        e1 = floatx4s{0.f, 0.f, 0.f, 0.f};
     }
     const int col = nb + wn * 16 + li;
     if (col >= N) return;
@@ -1681,6 +1721,36 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
             C[o] = shpd::apply_act(v, act, alpha);
         }
     }
+}
+
+// K-splits of the small-product path for an [M][K] x [N][K]^T product (0: not taken).  K <=
+// 256 runs unsplit where the 64x64 tiles would give fewer than 512 workgroups; a longer K (up
+// to 2,048) is cut into equal runs of at most 16 chunks, more of them (up to 8) while the
+// grid has fewer than 1,024 workgroups (swept over 2-8 splits on the MobileNetV2 and
+// EfficientNet-Lite0 projections: within 0.5 us of the best count).  `small` is the
+// gemm_small tune value: -1 never, 1 wherever the shape fits, k >= 2 with k splits.
+int small_gemm_splits(int64_t M, int64_t N, int K, int small) {
+    if (small < 0 || M <= 0 || N <= 0 || K <= 0 || K % 4 ||
+        K > 16 * kSmallKc * kSmallMaxSplits)
+        return 0;
+    if (M * K * 4 >= (1ll << 31) || N * K * 4 >= (1ll << 31)) return 0;
+    if (small == 0 && ((M + 63) / 64) * ((N + 63) / 64) >= 512) return 0;
+    const int kc = (K + 15) / 16;
+    const int64_t tiles = ((M + 31) / 32) * ((N + 31) / 32);
+    if (tiles >= (1ll << 31)) return 0;
+    int sp = small >= 2 ? std::min(small, kSmallMaxSplits) : (kc + kSmallKc - 1) / kSmallKc;
+    if (small < 2 && kc > kSmallKc)
+        while (sp < kSmallMaxSplits && sp < kc && tiles * sp < 1024) ++sp;
+    const int cps = (kc + sp - 1) / sp;
+    if (cps > kSmallKc) return 0;
+    sp = (kc + cps - 1) / cps;  // every split gets at least one chunk
+    if (sp > 1 && tiles * (int64_t)sizeof(int) > (int64_t)shp::kSplitCounterBytes) return 0;
+    return sp;
+}
+size_t small_gemm_workspace(int64_t M, int64_t N, int splits) {
+    if (splits <= 1) return 0;
+    const int64_t tiles = ((M + 31) / 32) * ((N + 31) / 32);
+    return shp::kSplitCounterBytes + (size_t)tiles * splits * 256 * sizeof(float4);
 }
 
 // ---- fully_connected with 2-16 rows (fc_mfma_kernel): y[M][N] = x[M][K] W[N][K]^T + bias
@@ -2274,10 +2344,15 @@ size_t gemm_workspace_for_kernel(const char* name, const int32_t* q, size_t n,
         return 0;
     }
     if (p.M <= 0 || p.N <= 0 || p.K <= 0) return 0;
+    size_t small_ws = 0;  // the K-split small-product path of a 1x1 conv2d_nhwc
+    if (k == "conv2d_nhwc" && q[7] == 1 && q[8] == 1 && q[9] == 1 && q[10] == 1 &&
+        q[12] == 0 && q[13] == 0 && q[5] == q[2] && q[6] == q[3])
+        small_ws = small_gemm_workspace(p.M, p.N,
+                                        small_gemm_splits(p.M, p.N, p.K, tune ? tune->small : 0));
     const int cm = k == "conv2d" ? C_NCHW : C_STRIDED;
     // and the generic plan too, so a launch whose bindings turn out unaligned finds its partials
-    return std::max(gemm_workspace_bytes(p, am, bm, cm, tune),
-                    gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED, tune));
+    return std::max({gemm_workspace_bytes(p, am, bm, cm, tune),
+                     gemm_workspace_bytes(p, A_STRIDED, B_STRIDED, C_STRIDED, tune), small_ws});
 }
 
 // Band height of the tile order (GemmParams::group_m, see wg_coords).  For each candidate
@@ -2488,31 +2563,28 @@ int conv2d_common(const shp::Launch& l, bool nhwc) {
         if (rc != SHP_ERR_UNSUPPORTED) return rc;
     }
     // 1x1 stride-1 unpadded NHWC convolutions are plain [M][K] x [N][K]^T products: the
-    // small-product kernel where K <= 256 and the 64x64 tiles would not fill the GPU
+    // small-product kernel where the 64x64 tiles would not fill the GPU (K-split past 256)
     const int small = l.tune ? l.tune->small : 0;
-    if (nhwc && small >= 0 && q[7] == 1 && q[8] == 1 && q[9] == 1 && q[10] == 1 && q[12] == 0 &&
-        q[13] == 0 && q[5] == q[2] && q[6] == q[3] && p.K % 4 == 0 && p.K <= 16 * kSmallKc &&
-        al16(p.a) && al16(p.b) && (int64_t)p.M * p.K * 4 < (1ll << 31) &&
-        (int64_t)p.N * p.K * 4 < (1ll << 31) &&
-        (small > 0 || (int64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) < 512)) {
+    const int ssp = nhwc && q[7] == 1 && q[8] == 1 && q[9] == 1 && q[10] == 1 && q[12] == 0 &&
+                            q[13] == 0 && q[5] == q[2] && q[6] == q[3] && al16(p.a) && al16(p.b)
+                        ? small_gemm_splits(p.M, p.N, p.K, small)
+                        : 0;
+    if (ssp == 1 || (ssp > 1 && l.workspace &&
+                     l.workspace_bytes >= small_gemm_workspace(p.M, p.N, ssp))) {
         const int tiles_n = (p.N + 31) / 32;
         const int64_t grid = (int64_t)((p.M + 31) / 32) * tiles_n;
-        if (grid < (1ll << 31)) {
-            const int kc = (p.K + 15) / 16;
-            const size_t lds = (size_t)64 * small_gemm_kp(kc) * sizeof(float);
-            auto kern = kc <= 2 ? small_gemm_kernel<2>
-                      : kc <= 4 ? small_gemm_kernel<4>
-                      : kc <= 8 ? small_gemm_kernel<8>
-                      : kc <= 12 ? small_gemm_kernel<12> : small_gemm_kernel<kSmallKc>;
-            if (lds > 64 * 1024)
-                SHP_HIP_CHECK(hipFuncSetAttribute((const void*)kern,
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  (int)lds));
-            hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), lds, l.stream, p.a, p.b,
-                               p.c, p.M, p.N, p.K, tiles_n, p.bias, p.residual, p.act, p.alpha);
-            SHP_HIP_CHECK(hipGetLastError());
-            return SHP_OK;
-        }
+        const int cps = ((p.K + 15) / 16 + ssp - 1) / ssp;
+        auto kern = cps <= 2 ? small_gemm_kernel<2>
+                  : cps <= 4 ? small_gemm_kernel<4>
+                  : cps <= 8 ? small_gemm_kernel<8>
+                  : cps <= 12 ? small_gemm_kernel<12> : small_gemm_kernel<kSmallKc>;
+        float* part = ssp > 1 ? l.workspace + shp::kSplitCounterBytes / sizeof(float) : nullptr;
+        int* counters = ssp > 1 ? reinterpret_cast<int*>(l.workspace) : nullptr;
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid, (unsigned)ssp), dim3(256), 0, l.stream,
+                           p.a, p.b, p.c, p.M, p.N, p.K, tiles_n, p.bias, p.residual, p.act,
+                           p.alpha, part, counters);
+        SHP_HIP_CHECK(hipGetLastError());
+        return SHP_OK;
     }
     int bm = (p.K % 4 == 0 && al16(p.b)) ? shp::B_KVEC : shp::B_STRIDED;
     if (nhwc) {

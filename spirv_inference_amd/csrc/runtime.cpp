@@ -326,7 +326,7 @@ int shp_workspace_info(shp_ctx* ctx, void** dptr, uint64_t* bytes) {
 // gemm_sk, gemm_stem, gemm_group, dw_tile; the fused block's ir_th, ir_tw, ir_splits,
 // ir_cout_splits and the model graphs' ir_fuse; conv_direct (-1: small-channel 3x3
 // conv2d_nhwc on the implicit GEMM instead of the direct kernel); gemm_small (1x1 conv2d_nhwc
-// with K <= 256 on the small-product kernel: 1 wherever it fits, -1 never); fc_mfma (-1:
+// on the small-product kernel: 1 wherever it fits, k >= 2 with k K-splits, -1 never); fc_mfma (-1:
 // fully_connected with 2-16 rows on the wavefront-per-column or tiled kernels).
 int shp_tune(shp_ctx* ctx, const char* key, int value) {
     if (!ctx) return fail(SHP_ERR_INVALID, "shp_tune: null ctx");

@@ -706,23 +706,29 @@ def test_conv2d_nhwc_direct_small_channels(ctx, orc, n, ic, h, w, oc, s, act, re
         assert not np.array_equal(y, y0), "the direct kernel did not run"
 
 
-@pytest.mark.parametrize("n,ic,h,w,oc,act,res", [
-    (8, 112, 14, 14, 672, "relu6", False),   # EfficientNet-Lite0 b8 block 9 expand
-    (8, 192, 7, 7, 1152, "relu6", False),    # block 12 expand
-    (3, 20, 5, 7, 36, None, True),           # partial 32x32 tiles, residual
-    (2, 4, 9, 9, 8, "relu", False),          # one K quarter
-    (2, 24, 11, 13, 144, "relu6", False),    # two chunks, the second partly past K
-    (1, 80, 14, 14, 480, "relu6", True),     # five chunks of the eight-chunk variant
-    (1, 240, 3, 5, 70, None, True),          # fifteen chunks
-    (1, 256, 6, 6, 40, None, True)],         # K at the limit (LDS beyond 64 KiB)
+@pytest.mark.parametrize("n,ic,h,w,oc,act,res,force", [
+    (8, 112, 14, 14, 672, "relu6", False, 1),   # EfficientNet-Lite0 b8 block 9 expand
+    (8, 192, 7, 7, 1152, "relu6", False, 1),    # block 12 expand
+    (3, 20, 5, 7, 36, None, True, 1),           # partial 32x32 tiles, residual
+    (2, 4, 9, 9, 8, "relu", False, 1),          # one K quarter
+    (2, 24, 11, 13, 144, "relu6", False, 1),    # two chunks, the second partly past K
+    (1, 80, 14, 14, 480, "relu6", True, 1),     # five chunks of the eight-chunk variant
+    (1, 240, 3, 5, 70, None, True, 1),          # fifteen chunks
+    (1, 256, 6, 6, 40, None, True, 1),          # one split's limit (LDS beyond 64 KiB)
+    (8, 1152, 7, 7, 320, None, False, 0),       # EfficientNet-Lite0 b8 block 15 projection: K split
+    (1, 960, 7, 7, 160, None, True, 0),         # MobileNetV2 b1 block 14 projection, residual
+    (2, 300, 5, 5, 37, "relu", False, 1),       # K 300: 19 chunks in two runs, ragged tiles
+    (2, 2048, 3, 3, 24, None, True, 1),         # K at the limit: 8 runs of 16 chunks
+    (3, 80, 6, 5, 40, "relu6", True, 3)],       # a short K forced into three runs
     ids=["effnet-b9-expand", "effnet-b12-expand", "odd-res", "k4", "k24", "k80", "k240",
-         "k256"])
-def test_conv2d_nhwc_1x1_small_kernel(ctx, orc, n, ic, h, w, oc, act, res):
-    """1x1 conv2d_nhwc with K <= 256 on the small-product kernel (32x32 tiles, operands
-    staged through LDS in 16-wide K chunks, each multiplied as it lands): against the oracle,
-    and against the tiled GEMM with the small kernel switched off (both agree with the oracle;
-    their K orders differ, so some outputs differ in the last bits, which shows the small
-    kernel ran)."""
+         "k256", "effnet-b15-project", "mbv2-b14-project", "k300", "k2048", "k80-split3"])
+def test_conv2d_nhwc_1x1_small_kernel(ctx, orc, n, ic, h, w, oc, act, res, force):
+    """1x1 conv2d_nhwc on the small-product kernel (32x32 tiles, operands staged through LDS in
+    16-wide K chunks, each multiplied as it lands; past 256, K cut into runs whose partial tiles
+    the last-arriving workgroup sums): against the oracle, and against the tiled GEMM with the
+    small kernel switched off (both agree with the oracle; their K orders differ, so some
+    outputs differ in the last bits, which shows the small kernel ran).  Two launches in a row
+    check that the split-K tile counters are left at zero."""
     total = n * h * w * oc
     push = [n, ic, h, w, oc, h, w, 1, 1, 1, 1, 1, 0, 0, total]
     wt = np.concatenate([rnd(oc * ic, scale=float(np.sqrt(2.0 / ic))), rnd(oc, scale=0.1)])
@@ -731,13 +737,15 @@ def test_conv2d_nhwc_1x1_small_kernel(ctx, orc, n, ic, h, w, oc, act, res):
     if res:
         kw["residual"] = rnd(total)
     try:
-        _tune(ctx, "gemm_small", 1)
+        _tune(ctx, "gemm_small", force)
+        y2 = hip(ctx, "conv2d_nhwc", x, wt, total, push, **kw)
         y, r = both(ctx, orc, "conv2d_nhwc", x, wt, total, push, **kw)
         _tune(ctx, "gemm_small", -1)
         y0 = hip(ctx, "conv2d_nhwc", x, wt, total, push, **kw)
     finally:
         _tune(ctx, "gemm_small", 0)
     assert_close(y, r, 1e-4, 1e-4, f"small 1x1 conv {push[:7]}")
+    assert y.tobytes() == y2.tobytes(), "repeat launch differs"
     assert_close(y0, r, 1e-4, 1e-4, f"tiled 1x1 conv {push[:7]}")
     if total >= 4096:
         assert not np.array_equal(y, y0), "the small kernel did not run"
