@@ -670,7 +670,7 @@ const TunedBlock kTunedBlocks[] = {
     {1, 96, 14, 14, 576, 96, 3, 1, 1, 8, 2, 16, 2, true},     // block11-12: 14.6 / 19.9
     {1, 96, 14, 14, 576, 160, 3, 2, 1, 7, 1, 16, 4, true},    // block13: 14.6 / 19.9
     {1, 160, 7, 7, 960, 160, 3, 1, 1, 4, 4, 16, 3, true},     // block14-15: 16.8 / 21.7
-    {1, 160, 7, 7, 960, 320, 3, 1, 1, 7, 2, 16, 3, true},     // block16: 18.8 / 21.9
+    {1, 160, 7, 7, 960, 320, 3, 1, 1, 7, 2, 16, 3, false},    // block16: 18.7 / 16.3
     // EfficientNet-Lite0 batch 8
     {8, 32, 112, 112, 32, 16, 3, 1, 0, 8, 7, 1, 1, true},     // block0: 24.6 / 29.5
     {8, 16, 112, 112, 96, 24, 3, 2, 1, 7, 4, 1, 1, true},     // block1: 32.5 / 42.7
@@ -689,7 +689,7 @@ const TunedBlock kTunedBlocks[] = {
     {8, 480, 14, 14, 480, 80, 3, 1, 0, 7, 2, 4, 1, true},     // block6-7: 15.6 / 16.5
     {8, 480, 14, 14, 480, 112, 5, 1, 0, 8, 2, 4, 1, true},    // block8: 16.7 / 19.8
     {8, 672, 14, 14, 672, 112, 5, 1, 0, 8, 2, 4, 1, true},    // block9-10: 20.7 / 22.9
-    {8, 672, 14, 14, 672, 192, 5, 2, 0, 7, 2, 8, 2, true},    // block11: 16.1 / 16.8
+    {8, 672, 14, 14, 672, 192, 5, 2, 0, 7, 2, 8, 2, false},   // block11: 16.0 / 15.4
     {8, 1152, 7, 7, 1152, 192, 5, 1, 0, 7, 2, 8, 2, true},    // block12-14: 19.0 / 19.6
     {8, 1152, 7, 7, 1152, 320, 3, 1, 0, 7, 4, 8, 4, false},   // block15: 23.5 / 17.9
 };
