@@ -48,6 +48,7 @@ constexpr int ES = CC + 1;   // LDS row stride (floats) of the expanded chunk
 constexpr int DS = CC + 4;   // of the depthwise chunk: 16-byte rows, 4 banks apart
 constexpr int WPS = CC + 4;  // of the projection weight chunk
 constexpr int NPF = 12;      // float4 weight loads per thread and chunk, at most
+constexpr int NPF_DP = 6;    // the same without expand, where two chunks' sets are in flight
 constexpr int kMaxLds = 160 * 1024;
 
 // LDS layout (float offsets) of one workgroup, shared by the host plan and the kernel:
@@ -140,23 +141,23 @@ __device__ __forceinline__ void weight_slot(const IrArgs& a, const IrLds& L, int
 // Loads (fetch) and LDS stores (put) of this thread's float4s of one chunk's weights,
 // unrolled by recursion so the staging registers stay registers.  Channels past ce (the
 // second half of a 16-channel last chunk) read as zeros.
-template <int U>
-__device__ __forceinline__ void fetch_weights(f4v (&pf)[NPF], const IrArgs& a,
+template <int U, int N>
+__device__ __forceinline__ void fetch_weights(f4v (&pf)[N], const IrArgs& a,
                                               __amdgpu_buffer_rsrc_t wr, const int (&goff)[NPF],
                                               const int (&meta)[NPF], int tid, int nf, int ch) {
-    if constexpr (U < NPF) {
+    if constexpr (U < N) {
         const bool ok = (tid + 256 * U < nf) & (ch * CC + ((meta[U] >> 16) & 255) < a.ce);
         const int stp = (meta[U] >> 24) ? CC * a.cin : CC;
         pf[U] = ld16(wr, ok ? (unsigned)(goff[U] + stp * ch) * 4u : kOob);
-        fetch_weights<U + 1>(pf, a, wr, goff, meta, tid, nf, ch);
+        fetch_weights<U + 1, N>(pf, a, wr, goff, meta, tid, nf, ch);
     }
 }
-template <int U>
-__device__ __forceinline__ void put_weights(const f4v (&pf)[NPF], float* lds,
+template <int U, int N>
+__device__ __forceinline__ void put_weights(const f4v (&pf)[N], float* lds,
                                             const int (&meta)[NPF], int tid, int nf) {
-    if constexpr (U < NPF) {
+    if constexpr (U < N) {
         if (tid + 256 * U < nf) *reinterpret_cast<f4v*>(lds + (meta[U] & 0xFFFF)) = pf[U];
-        put_weights<U + 1>(pf, lds, meta, tid, nf);
+        put_weights<U + 1, N>(pf, lds, meta, tid, nf);
     }
 }
 
@@ -180,8 +181,9 @@ __device__ __forceinline__ floatx4 mfma4(f4v a, f4v b, floatx4 c) {
 // K, ST: depthwise kernel size and stride; NBW: projection blocks (16 pixels x 16 output
 // channels) per wavefront, at most; EXP: the block has an expand (a.expand, as a constant).
 // Without one the input already has the expanded channels: each chunk's 32 of them are staged
-// over the halo from x (UH float4 per thread, loaded during the previous chunk), so the LDS
-// never holds all channels and the depthwise reads them as it reads E.
+// over the halo from x (UH float4 per thread, loaded two chunks ahead with the chunk's weights,
+// in two register sets), so the LDS never holds all channels and the depthwise reads them as it
+// reads E.
 constexpr int UH = 5;  // halo float4 per thread per chunk without expand: 8 * hpb * 16 <= 256 * UH
 template <int K, int ST, int NBW, bool EXP>
 __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
@@ -244,8 +246,8 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
             if (xd[t] >= 0) *reinterpret_cast<f4v*>(Xs + xd[t]) = xv[t];
     };
     // without expand: the chunk's 32 channels of the halo, 8 float4 per halo row
-    f4v hq[UH];
-    auto load_h = [&](int ch) {
+    f4v hq[UH], hq2[UH];
+    auto load_h = [&](f4v (&hh)[UH], int ch) {
 #pragma unroll
         for (int u = 0; u < UH; ++u) {
             const int e = tid + 256 * u;
@@ -254,24 +256,28 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
             const int iy = iy0 + hy, ix = ix0 + hx;
             const bool in = (r < a.hp) & (c < a.cin) & ((unsigned)iy < (unsigned)a.h) &
                             ((unsigned)ix < (unsigned)a.w_);
-            hq[u] = ld16(xr, in ? (unsigned)((iy * a.w_ + ix) * a.cin + c) * 4u : kOob);
+            hh[u] = ld16(xr, in ? (unsigned)((iy * a.w_ + ix) * a.cin + c) * 4u : kOob);
         }
     };
-    auto store_h = [&]() {
+    auto store_h = [&](const f4v (&hh)[UH]) {
 #pragma unroll
         for (int u = 0; u < UH; ++u) {
             const int e = tid + 256 * u;
             if (e < hrows * 8) {
                 float* d = Es + (e >> 3) * ES + 4 * (e & 7);  // rows 33 floats apart
 #pragma unroll
-                for (int i = 0; i < 4; ++i) d[i] = hq[u][i];
+                for (int i = 0; i < 4; ++i) d[i] = hh[u][i];
             }
         }
     };
+    // Without expand every chunk load is issued unconditionally, so the wait counts do not
+    // depend on the path: a chunk past this split's end is asked for as chunk nchunk, which
+    // lies past ce and reads zeros without a memory access.
+    const int c_none = a.nchunk;
     if (EXP)
         load_x(tid);
-    else if (c_begin < c_end)
-        load_h(c_begin);
+    else
+        load_h(hq, c_begin < c_end ? c_begin : c_none);
 
     // this thread's share of every chunk's weights, and the first chunk's loads
     int goff[NPF], meta[NPF];
@@ -280,10 +286,19 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
         goff[u] = meta[u] = 0;
         if (tid + 256 * u < nf) weight_slot<K>(a, L, j, tid + 256 * u, goff[u], meta[u]);
     }
-    f4v pf[NPF];  // (native vectors: HIP's float4 struct copies would pin them to scratch)
+    // (native vectors: HIP's float4 struct copies would pin them to scratch)
+    f4v pf[EXP ? NPF : NPF_DP];
     const __amdgpu_buffer_rsrc_t wr =
         buffer_rsrc(a.w, a.w_wd + (int64_t)(K * K + 1 + a.cout) * a.ce + a.cout);
     fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, c_begin < c_end ? c_begin : 0);
+    // without expand the next chunk's halo and weights load too (a second register set): each
+    // chunk's loads go out two chunks ahead of its use
+    f4v pf2[EXP ? 1 : NPF_DP];
+    if (!EXP) {
+        const int c1 = c_begin + 1 < c_end ? c_begin + 1 : c_none;
+        load_h(hq2, c1);
+        fetch_weights<0>(pf2, a, wr, goff, meta, tid, nf, c1);
+    }
 
     if (EXP) {
         store_x();
@@ -312,16 +327,7 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
     for (int i = 0; i < NBW; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int dc = tid & 31, dy = tid >> 5;  // depthwise: channel and output row of the tile
-    for (int ch = c_begin; ch < c_end; ++ch) {
-        __syncthreads();  // the previous chunk's readers are done with its weights, E and D
-        put_weights<0>(pf, lds, meta, tid, nf);
-        if (!EXP) {
-            store_h();
-            if (ch + 1 < c_end) load_h(ch + 1);
-        }
-        if (ch + 1 < c_end)  // the next chunk's weights load while this one computes
-            fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, ch + 1);
-        __syncthreads();
+    auto body = [&](int ch) {  // one staged chunk: expand, depthwise, projection
         const int c0 = ch * CC;
         const bool half = c0 + 16 >= a.ce;  // a 16-channel last chunk: one column block
         if (EXP) {
@@ -433,6 +439,35 @@ __global__ __launch_bounds__(256) void ir_kernel(IrArgs a) {
                                *reinterpret_cast<const f4v*>(wp + 4), acc[i]);
             }
         }
+    };
+    if constexpr (EXP) {
+        for (int ch = c_begin; ch < c_end; ++ch) {
+            __syncthreads();  // the previous chunk's readers are done with its weights, E and D
+            put_weights<0>(pf, lds, meta, tid, nf);
+            if (ch + 1 < c_end)  // the next chunk's weights load while this one computes
+                fetch_weights<0>(pf, a, wr, goff, meta, tid, nf, ch + 1);
+            __syncthreads();
+            body(ch);
+        }
+    } else {
+        // chunks in pairs, the first of a pair from set 1 (pf, hq) and the second from set 2
+        // (pf2, hq2); a set, once stored, loads the chunk two ahead
+        auto step = [&](f4v (&hh)[UH], f4v (&pp)[NPF_DP], int ch) {
+            __syncthreads();  // the previous chunk's readers are done with its weights and D
+            put_weights<0>(pp, lds, meta, tid, nf);
+            store_h(hh);
+            const int cn = ch + 2 < c_end ? ch + 2 : c_none;
+            load_h(hh, cn);
+            fetch_weights<0>(pp, a, wr, goff, meta, tid, nf, cn);
+            __syncthreads();
+            body(ch);
+        };
+        int ch = c_begin;
+        for (; ch + 1 < c_end; ch += 2) {
+            step(hq, pf, ch);
+            step(hq2, pf2, ch + 1);
+        }
+        if (ch < c_end) step(hq, pf, ch);
     }
 
     // Output position (projection block b, lane l): 4 pixels of one output channel.  Its
@@ -610,7 +645,8 @@ IrGeom geometry(const IrShape& sh, int th, int tw, int S, int J) {
 }
 
 bool geometry_ok(const IrGeom& g) {
-    return g.lds_floats * 4 <= kMaxLds && g.nbw <= 20 && g.nf_max <= 256 * NPF &&
+    return g.lds_floats * 4 <= kMaxLds && g.nbw <= 20 &&
+           g.nf_max <= 256 * (g.expand ? NPF : NPF_DP) &&
            (g.expand || g.hpb * 16 * 8 <= 256 * UH) &&  // the halo chunk's float4 per thread
            (int64_t)g.S * g.nblk * 1024 < (1ll << 31) &&
            // the kernel's multiply-high divisions of the workgroup id stay exact
