@@ -712,7 +712,7 @@ const TunedBlock kTunedBlocks[] = {
     {8, 16, 112, 112, 96, 24, 3, 2, 1, 7, 4, 1, 1, true},     // block1: 32.5 / 42.7
     {8, 24, 56, 56, 144, 24, 3, 1, 1, 8, 7, 1, 1, true},      // block2: 27.2 / 43.5
     {8, 24, 56, 56, 144, 40, 5, 2, 1, 7, 2, 1, 1, true},      // block3: 24.6 / 41.6
-    {8, 40, 28, 28, 240, 40, 5, 1, 1, 7, 7, 4, 1, true},      // block4: 23.6 / 40.1
+    {8, 40, 28, 28, 240, 40, 5, 1, 1, 7, 7, 4, 1, false},     // block4: 24.0 / 28.2
     {8, 40, 28, 28, 240, 80, 3, 2, 1, 8, 2, 4, 1, true},      // block5: 17.4 / 27.5
     {8, 80, 14, 14, 480, 80, 3, 1, 1, 7, 4, 8, 1, false},     // block6-7: 22.6 / 25.6
     {8, 80, 14, 14, 480, 112, 5, 1, 1, 4, 4, 4, 1, false},    // block8: 26.3 / 29.5
@@ -722,6 +722,7 @@ const TunedBlock kTunedBlocks[] = {
     {8, 192, 7, 7, 1152, 320, 3, 1, 1, 7, 4, 8, 2, false},    // block15: 42.7 / 27.8
     // EfficientNet-Lite0 batch 8, the blocks above that do not fuse whole: depthwise +
     // projection as one launch after the expand GEMM (us: one launch / two launches)
+    {8, 240, 28, 28, 240, 40, 5, 1, 0, 8, 4, 2, 1, true},     // block4: 16.2 / 21.0
     {8, 480, 14, 14, 480, 80, 3, 1, 0, 7, 2, 4, 1, true},     // block6-7: 15.6 / 16.5
     {8, 480, 14, 14, 480, 112, 5, 1, 0, 8, 2, 4, 1, true},    // block8: 16.7 / 19.8
     {8, 672, 14, 14, 672, 112, 5, 1, 0, 8, 2, 4, 1, true},    // block9-10: 20.7 / 22.9
