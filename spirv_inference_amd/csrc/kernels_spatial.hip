@@ -493,15 +493,10 @@ __global__ __launch_bounds__(256) void conv_direct_nhwc_kernel(const float* __re
     constexpr int KK = KH * KW;
     constexpr int K = KK * CI;
     const int tid = threadIdx.x;
-    for (int e = tid; e < K * d.oc; e += 256) {  // OHWI -> [k][oc]
-        const int o = e / K, k = e - o * K;
-        cw[k * d.oc + o] = w[e];
-    }
-    for (int e = tid; e < d.oc; e += 256) cw[K * d.oc + e] = w[K * d.oc + e];
-    __syncthreads();
+    // this thread's inputs load first, so their round trip overlaps the weight staging's
     const int idx = blockIdx.x * 256 + tid;
-    if (idx >= d.total) return;
-    const int pix = udiv_mh(idx, d.m_ocg), g = idx - pix * d.ocg;
+    const bool live = idx < d.total;
+    const int pix = udiv_mh(live ? idx : 0, d.m_ocg), g = (live ? idx : 0) - pix * d.ocg;
     const int q = udiv_mh(pix, d.m_ow), ox = pix - q * d.ow;
     const int img = udiv_mh(q, d.m_oh), oy = q - img * d.oh;
     const int iy0 = oy * d.sh - d.pt, ix0 = ox * d.sw - d.pl;
@@ -519,6 +514,13 @@ __global__ __launch_bounds__(256) void conv_direct_nhwc_kernel(const float* __re
             v[t * CI + c] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(xr, off + 4u * c, 0u, 0));
     }
+    for (int e = tid; e < K * d.oc; e += 256) {  // OHWI -> [k][oc]
+        const int o = e / K, k = e - o * K;
+        cw[k * d.oc + o] = w[e];
+    }
+    for (int e = tid; e < d.oc; e += 256) cw[K * d.oc + e] = w[K * d.oc + e];
+    __syncthreads();
+    if (!live) return;
     const float* wg = cw + 8 * g;
     f4v a0 = *reinterpret_cast<const f4v*>(wg + K * d.oc);
     f4v a1 = *reinterpret_cast<const f4v*>(wg + K * d.oc + 4);
