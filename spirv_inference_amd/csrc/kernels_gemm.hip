@@ -1727,7 +1727,8 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
 // 256 runs unsplit where the 64x64 tiles would give fewer than 512 workgroups; a longer K (up
 // to 2,048) is cut into equal runs of at most 16 chunks, more of them (up to 8) while the
 // grid has fewer than 1,024 workgroups (swept over 2-8 splits on the MobileNetV2 and
-// EfficientNet-Lite0 projections: within 0.5 us of the best count).  `small` is the
+// EfficientNet-Lite0 projections: within 0.5 us of the best count; the same growth for K <= 256
+// split the EfficientNet-Lite0 b8 expands and cost that forward 11 us).  `small` is the
 // gemm_small tune value: -1 never, 1 wherever the shape fits, k >= 2 with k splits.
 int small_gemm_splits(int64_t M, int64_t N, int K, int small) {
     if (small < 0 || M <= 0 || N <= 0 || K <= 0 || K % 4 ||
