@@ -1463,7 +1463,25 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
     const bool vec = (K % 4 == 0) && (((uintptr_t)w & 15) == 0) && (((uintptr_t)x & 15) == 0);
-    if (vec) {
+    if (MR == 1 && vec && K <= 2048) {
+        // one row: every weight and activation load of the lane (up to eight 256-wide K
+        // steps) goes out before the first product, one round trip; the sums run in K order
+        // as below
+        float4 wv[8], xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int k = lane * 4 + 256 * j;
+            if (k < K) {
+                wv[j] = *reinterpret_cast<const float4*>(wr + k);
+                xv[j] = *reinterpret_cast<const float4*>(x + k);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (lane * 4 + 256 * j < K)
+                acc[0] += wv[j].x * xv[j].x + wv[j].y * xv[j].y + wv[j].z * xv[j].z +
+                          wv[j].w * xv[j].w;
+    } else if (vec) {
         // four 256-wide K steps' weight loads go out together (one HBM round trip per four
         // steps, not per step); the sums still run in K order
         for (int k0 = lane * 4; k0 < K; k0 += 1024) {
