@@ -1071,6 +1071,12 @@ __global__ __launch_bounds__(64 * NWV) void conv1x1_gap_small_kernel(const float
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(x + (int64_t)img * hw * cin, (int64_t)hw * cin);
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(w, (int64_t)cout * cin + cout);
     const int nch = (cin + 15) >> 4;
+    float biasv[CB];  // the epilogue's biases load with the operands
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int col = c0 + cb * 16 + li;
+        biasv[cb] = col < cout ? w[(int64_t)cout * cin + col] : 0.f;
+    }
     f4v xa[NK][4], wb[NK][CB];
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
@@ -1111,8 +1117,7 @@ __global__ __launch_bounds__(64 * NWV) void conv1x1_gap_small_kernel(const float
     if (rb < 4) {
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-        const int col = c0 + cb * 16 + li;
-        const float bias = col < cout ? w[(int64_t)cout * cin + col] : 0.f;
+        const float bias = biasv[cb];
         f4v v = red[0][rb][cb][lane];
 #pragma unroll
         for (int u = 1; u < NWV; ++u) v += red[u][rb][cb][lane];

@@ -1459,6 +1459,7 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
     const float* wr = w + (int64_t)n * K;
+    const float bn = bias ? bias[n] : 0.0f;  // loaded with the weights, used by lane 0
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
@@ -1516,10 +1517,8 @@ __global__ __launch_bounds__(256) void skinny_nt_kernel(const float* __restrict_
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
         acc[m] = v;
     }
-    if (lane == 0) {
-        float b = bias ? bias[n] : 0.0f;
-        for (int m = 0; m < M; ++m) y[(int64_t)m * N + n] = shpd::apply_act(acc[m] + b, act, alpha);
-    }
+    if (lane == 0)
+        for (int m = 0; m < M; ++m) y[(int64_t)m * N + n] = shpd::apply_act(acc[m] + bn, act, alpha);
 }
 
 // The same product for 2..8 rows with the rows staged in LDS once per workgroup: each
@@ -1686,6 +1685,17 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
                                                                         : kOobOffset,
                              0u);
     const int wm = wave >> 1, wn = wave & 1;
+    // the epilogue's bias and residuals load with the operands, not after the products
+    const int col = nb + wn * 16 + li;
+    const float bv = bias && col < N ? bias[col] : 0.0f;
+    float rv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (res && col < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = mb + wm * 16 + 4 * g + r;
+            if (m < M) rv[r] = res[(int64_t)m * N + col];
+        }
+    }
     const int fa = (wm * 16 + li) * kSmallRs + 4 * g;
     const int fb = (32 + wn * 16 + li) * kSmallRs + 4 * g;
     floatx4s e0 = {0.f, 0.f, 0.f, 0.f}, e1 = e0;
@@ -1726,16 +1736,14 @@ __global__ __launch_bounds__(256) void small_gemm_kernel(const float* __restrict
         e0 = floatx4s{t.x, t.y, t.z, t.w};
         e1 = floatx4s{0.f, 0.f, 0.f, 0.f};
     }
-    const int col = nb + wn * 16 + li;
     if (col >= N) return;
-    const float bv = bias ? bias[col] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {  // accumulator r: row 4g + r of the block, column li
         const int m = mb + wm * 16 + 4 * g + r;
         if (m < M) {
             const int64_t o = (int64_t)m * N + col;
             float v = e0[r] + e1[r] + bv;
-            if (res) v += res[o];
+            if (res) v += rv[r];
             C[o] = shpd::apply_act(v, act, alpha);
         }
     }
@@ -1796,6 +1804,12 @@ __global__ __launch_bounds__(kFcWaves * 64) void fc_mfma_kernel(
     const bool xok = li < M, wok = n0 + li < N;
     const unsigned xb = (unsigned)(li * K + 4 * g) * 4u;
     const unsigned wb = (unsigned)((n0 + li) * K + 4 * g) * 4u;
+    // the epilogue's bias and residual (thread tid < 256: row tid / 16, column tid % 16) load
+    // with the operands
+    const int orow = tid >> 4, ocol = n0 + (tid & 15);
+    const bool oown = tid < 256 && orow < M && ocol < N;
+    const float obias = oown && bias ? bias[ocol] : 0.0f;
+    const float ores = oown && res ? res[(int64_t)orow * N + ocol] : 0.0f;
     f4v a[CPW], b[CPW];
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
@@ -1822,11 +1836,10 @@ __global__ __launch_bounds__(kFcWaves * 64) void fc_mfma_kernel(
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < kFcWaves; ++w) v += red[(w * 4 + r) * 64 + l];
-        if (row < M && n0 + col < N) {
-            const int64_t o = (int64_t)row * N + n0 + col;
-            v += bias ? bias[n0 + col] : 0.0f;
-            if (res) v += res[o];
-            Y[o] = shpd::apply_act(v, act, alpha);
+        if (oown) {
+            v += obias;
+            if (res) v += ores;
+            Y[(int64_t)row * N + n0 + col] = shpd::apply_act(v, act, alpha);
         }
     }
 }
